@@ -1,0 +1,298 @@
+"""Benchmark of the gfx950 FlashAttention-2 forward (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A "step" is one call of the public entry point on one batch of synthetic
+input already resident in HBM.  The default workload is BASELINE config 2,
+the metric's headline shape: dense FP16 causal forward, B=4, H=32,
+S_q=S_k=4096, D=128 (``flash_attn_func(q, k, v, causal=True)``).  Other
+workloads (``--workload``): ``dense`` (same shape, non-causal),
+``int8_causal`` / ``int8`` (config 3, ``attention_int8``, quantization
+prepass included), ``decode`` (config 4, paged GQA decode through
+``flash_attn_with_kvcache``) and ``varlen`` (config 5).
+
+FLOP convention (reference README.md:226-229): causal 2*B*H*D*S*(S+1),
+non-causal 4*B*H*D*S^2; varlen counts 4*H*D per unmasked (q, k) pair; decode
+is measured in algorithmic bytes (K/V rows read + q + out + block table).
+
+The JSON line carries ``roofline`` (the dominant kernel's algorithmic rate,
+timed with HIP events around each launch on the launch stream, against the
+MI355X published peak) and ``cpu_baseline`` (the float64 numpy oracle timed
+on a bounded sample of the same workload on the host cores).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "flash-attn-triton_amd"))
+sys.path.insert(0, ROOT)
+
+PEAK = {"fp16": 2500.0, "int8_mixed": 1.0 / (0.5 / 5000.0 + 0.5 / 2500.0), "hbm": 8000.0}
+
+
+def _randn(torch, shape, seed, dtype, device):
+    gen = torch.Generator(device=device).manual_seed(seed)
+    return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32).to(dtype)
+
+
+# ----------------------------------------------------------------------------- workloads
+def make_dense(torch, causal):
+    from flash_attn_triton import flash_attn_func
+    B, S, H, D = 4, 4096, 32, 128
+    q, k, v = (_randn(torch, (B, S, H, D), s, torch.float16, "cuda") for s in (1, 2, 3))
+    flops = 2.0 * B * H * D * S * (S + 1) if causal else 4.0 * B * H * D * S * S
+
+    def step():
+        return flash_attn_func(q, k, v, causal=causal)
+
+    def cpu(budget_s):
+        import numpy as np
+        from oracle import attention as ora
+        qc, kc, vc = (t[:1].cpu().numpy() for t in (q, k, v))
+        done, heads, t0 = 0.0, 0, time.perf_counter()
+        while heads < H and (time.perf_counter() - t0) < budget_s:
+            ora.attention(qc[:, :, heads:heads + 1], kc[:, :, heads:heads + 1],
+                          vc[:, :, heads:heads + 1], causal=causal)
+            heads += 1
+        dt = time.perf_counter() - t0
+        per_head = flops / (B * H)
+        return {"value": per_head * heads / dt / 1e12, "unit": "TFLOP/s",
+                "cores": os.cpu_count(), "kind": "port",
+                "sample": f"float64 numpy oracle (oracle/attention.py) on {heads} of {B * H} "
+                          f"(batch, head) pairs, S=4096, D=128, causal={causal}; "
+                          f"{dt:.1f} s; OpenBLAS threads = host cores"}
+
+    cfg = {"workload": f"dense_fp16_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
+           "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
+           "layout": "BSHD contiguous"}
+    return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="fp16",
+                metric="attn fwd TFLOP/s (FP16) S=4096 D=128", bound="mfma", peak=PEAK["fp16"],
+                peak_unit="TFLOP/s", config=cfg, cpu=cpu, kernel="fwd_kernel")
+
+
+def make_int8(torch, causal):
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import attention_int8
+    B, H, S, D = 4, 32, 4096, 128
+    q, k, v = (_randn(torch, (B, H, S, D), s, torch.float16, "cuda") for s in (4, 5, 6))
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    n_out = S // 100
+    idx = torch.argsort(torch.rand(B * H, S, generator=gen, device="cuda"), dim=1)[:, :n_out]
+    kf = k.view(B * H, S, D)
+    rows = torch.arange(B * H, device="cuda")[:, None].expand(-1, n_out)
+    kf[rows, idx] = (kf[rows, idx].float() * 8.0).half()
+    flops = 2.0 * B * H * D * S * (S + 1) if causal else 4.0 * B * H * D * S * S
+
+    def step():
+        return attention_int8(q, k, v, causal=causal)
+
+    def cpu(budget_s):
+        from oracle import quant
+        qc, kc, vc = (t[:1].cpu().numpy() for t in (q, k, v))
+        heads, t0 = 0, time.perf_counter()
+        while heads < H and (time.perf_counter() - t0) < budget_s:
+            quant.attention_int8(qc[:, heads:heads + 1], kc[:, heads:heads + 1],
+                                 vc[:, heads:heads + 1].astype("float64"), causal=causal)
+            heads += 1
+        dt = time.perf_counter() - t0
+        return {"value": flops / (B * H) * heads / dt / 1e12, "unit": "TFLOP/s",
+                "cores": os.cpu_count(), "kind": "port",
+                "sample": f"numpy INT8-QK oracle (oracle/quant.py) on {heads} of {B * H} "
+                          f"(batch, head) pairs, S=4096, D=128; {dt:.1f} s"}
+
+    cfg = {"workload": f"int8qk_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
+           "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
+           "k_outliers": "1% of token rows x8", "layout": "BHSD contiguous"}
+    return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="int8+fp16",
+                metric="attn fwd TFLOP/s (INT8-QK) S=4096 D=128", bound="mfma",
+                peak=PEAK["int8_mixed"], peak_unit="TFLOP/s", config=cfg, cpu=cpu,
+                kernel="int8_fwd_kernel")
+
+
+def make_decode(torch):
+    from flash_attn_triton import flash_attn_with_kvcache
+    B, Hq, Hk, D, page = 64, 32, 8, 128, 256
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(512, 8193, (B,), generator=gen)
+    pages_per = ((lengths + page - 1) // page).tolist()
+    n_pages = sum(pages_per)
+    perm = torch.randperm(n_pages, generator=gen)
+    bt = torch.zeros((B, 32), dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(pages_per):
+        bt[b, :n] = perm[pos:pos + n].to(torch.int32)
+        pos += n
+    kc = _randn(torch, (n_pages, page, Hk, D), 11, torch.float16, "cuda")
+    vc = _randn(torch, (n_pages, page, Hk, D), 12, torch.float16, "cuda")
+    q = _randn(torch, (B, 1, Hq, D), 13, torch.float16, "cuda")
+    seqlens = lengths.to(torch.int32).cuda()
+    btd = bt.cuda()
+    total_tokens = int(lengths.sum())
+    nbytes = (total_tokens * Hk * D * 2 * 2 + q.numel() * 2 * 2 + sum(pages_per) * 4 + B * 4)
+
+    def step():
+        return flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens, block_table=btd)
+
+    def cpu(budget_s):
+        from oracle import attention as ora
+        qn, kn, vn = q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy()
+        done_bytes, b, t0 = 0, 0, time.perf_counter()
+        while b < B and (time.perf_counter() - t0) < budget_s:
+            ora.attention_kvcache(qn[b:b + 1], kn, vn, cache_seqlens=[int(lengths[b])],
+                                  block_table=bt[b:b + 1].numpy())
+            done_bytes += int(lengths[b]) * Hk * D * 2 * 2
+            b += 1
+        dt = time.perf_counter() - t0
+        return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": os.cpu_count(),
+                "kind": "port",
+                "sample": f"float64 numpy oracle (gather through the block table + attention) on "
+                          f"{b} of {B} sequences; {dt:.1f} s"}
+
+    cfg = {"workload": "paged_decode_b64_hq32_hk8_d128_page256", "batch": B, "heads_q": Hq,
+           "heads_k": Hk, "head_dim": D, "page_size": page, "total_cache_tokens": total_tokens,
+           "cache_lengths": "U[512, 8192], seed 0", "block_table": "random page permutation"}
+    return dict(step=step, work=nbytes, unit="GB/s", scale=1e9, dtype="fp16",
+                metric="paged decode GB/s", bound="hbm", peak=PEAK["hbm"], peak_unit="GB/s",
+                config=cfg, cpu=cpu, kernel="fwd_kernel (kvcache split) + combine_kernel")
+
+
+def make_varlen(torch):
+    from flash_attn_triton import flash_attn_varlen_func
+    H, D = 16, 128
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(128, 4097, (32,), generator=gen)
+    cu = torch.zeros(33, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lengths, 0).to(torch.int32)
+    T = int(cu[-1])
+    q, k, v = (_randn(torch, (T, H, D), s, torch.float16, "cuda") for s in (21, 22, 23))
+    slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).float().cuda()
+    cud = cu.cuda()
+    max_len = int(lengths.max())
+
+    def pairs(L, left=1024):
+        i = torch.arange(L, dtype=torch.float64)
+        return float(torch.clamp(i, max=left).sum() + L)
+
+    n_pairs = sum(pairs(int(L)) for L in lengths)
+    flops = 4.0 * H * D * n_pairs
+
+    def step():
+        return flash_attn_varlen_func(q, k, v, cud, cud, max_len, max_len, causal=True,
+                                      window_size=(1024, 0), softcap=30.0, alibi_slopes=slopes)
+
+    def cpu(budget_s):
+        from oracle import attention as ora
+        qn, kn, vn = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+        sl = slopes.cpu().numpy()
+        done, b, t0 = 0.0, 0, time.perf_counter()
+        while b < 32 and (time.perf_counter() - t0) < budget_s:
+            s, e = int(cu[b]), int(cu[b + 1])
+            ora.attention(qn[None, s:e], kn[None, s:e], vn[None, s:e], None, True, (1024, 0),
+                          30.0, sl)
+            done += 4.0 * H * D * pairs(e - s)
+            b += 1
+        dt = time.perf_counter() - t0
+        return {"value": done / dt / 1e12, "unit": "TFLOP/s", "cores": os.cpu_count(),
+                "kind": "port",
+                "sample": f"float64 numpy oracle on {b} of 32 sequences; {dt:.1f} s"}
+
+    cfg = {"workload": "varlen_fp16_32seq_h16_d128_causal_win1024_alibi_softcap30",
+           "sequences": 32, "total_tokens": T, "heads": H, "head_dim": D,
+           "unmasked_pairs": n_pairs}
+    return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="fp16",
+                metric="varlen attn fwd TFLOP/s (FP16, causal+window+ALiBi+softcap)",
+                bound="mfma", peak=PEAK["fp16"], peak_unit="TFLOP/s", config=cfg, cpu=cpu,
+                kernel="fwd_kernel")
+
+
+WORKLOADS = {
+    "dense_causal": lambda torch: make_dense(torch, True),
+    "dense": lambda torch: make_dense(torch, False),
+    "int8_causal": lambda torch: make_int8(torch, True),
+    "int8": lambda torch: make_int8(torch, False),
+    "decode": make_decode,
+    "varlen": make_varlen,
+}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="dense_causal", choices=sorted(WORKLOADS))
+    ap.add_argument("--cpu-budget", type=float, default=12.0,
+                    help="seconds of host work for the CPU baseline sample (0 = skip)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one GPU; every box in this pipeline has one GPU and "
+              "the attention forward needs no cross-GPU exchange (see DESIGN.md for how it would "
+              "shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    torch.backends.cuda.matmul.allow_tf32 = False
+    wl = WORKLOADS[args.workload](torch)
+    step = wl["step"]
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
+    ms_per_step = wall / args.steps * 1e3
+    value = wl["work"] / (wall / args.steps) / wl["scale"]
+    achieved = wl["work"] / avg_launch_s / wl["scale"]
+
+    cpu = None
+    if args.cpu_budget > 0:
+        torch.set_num_threads(os.cpu_count() or 1)
+        cpu = wl["cpu"](args.cpu_budget)
+
+    line = {
+        "metric": wl["metric"],
+        "value": round(value, 3),
+        "unit": wl["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": wl["dtype"],
+        "data": "synthetic (seeded N(0,1))",
+        "config": wl["config"],
+        "roofline": {
+            "bound": wl["bound"],
+            "achieved": round(achieved, 3),
+            "peak": round(wl["peak"], 1),
+            "unit": wl["peak_unit"],
+            "frac": round(achieved / wl["peak"], 4),
+            "traffic": None,
+            "kernel": wl["kernel"],
+            "avg_launch_us": round(avg_launch_s * 1e6, 2),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

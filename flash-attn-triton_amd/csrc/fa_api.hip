@@ -1,0 +1,356 @@
+// C ABI of libfa_gfx950.so (declarations and contracts: include/fa_gfx950.h).
+//
+// Each entry point validates its arguments, fills a kernel parameter block
+// and launches on the caller's stream.  Nothing here allocates device memory
+// or synchronizes.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/fa_gfx950.h"
+#include "fa_fwd_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_last_error.clear();
+    return FA_OK;
+  }
+  return fail(FA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool supported_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
+
+// 16-byte vector loads need 16-byte aligned rows: base pointer aligned and
+// every stride a multiple of 8 two-byte elements.
+bool aligned16(const void* ptr, const int64_t* strides, int n) {
+  if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0) return false;
+  for (int i = 0; i < n; ++i)
+    if (strides[i] % 8 != 0) return false;
+  return true;
+}
+
+hipError_t launch_fwd(int dtype, const fa::FwdParams& p, int mode, int head_dim, bool generic,
+                      hipStream_t st) {
+  return dtype == FA_DTYPE_F16 ? fa_launch_fwd_f16(p, mode, head_dim, generic, st)
+                               : fa_launch_fwd_bf16(p, mode, head_dim, generic, st);
+}
+
+void fill_scale(fa::FwdParams& p, float scale, float softcap, const float* alibi) {
+  p.scale = scale;
+  p.scale_log2 = scale * fa::kLog2e;
+  p.softcap = softcap;
+  p.alibi = alibi;
+}
+
+bool needs_generic(const fa::FwdParams& p) {
+  return p.alibi != nullptr || p.softcap > 0.f || !(p.scale > 0.f);
+}
+
+struct KvPlan {
+  int num_splits, split_tiles;
+  int64_t o_part_bytes, lse_part_bytes;
+};
+
+KvPlan kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
+                    int64_t head_dim, int64_t max_keys) {
+  const int64_t group = heads_q / heads_k;
+  const int64_t rows = seqlen_q * group;
+  const int tile = fa::kvcache_tile_keys((int)rows, (int)head_dim);
+  const int64_t bm = (rows <= 32 && head_dim <= 128) ? 32 : 128;
+  const int64_t max_tiles = max_keys > 0 ? (max_keys + tile - 1) / tile : 1;
+  const int64_t base = batch * heads_k * ((rows + bm - 1) / bm);
+  // Enough workgroups to cover 256 CUs several times over; at least four key
+  // tiles per split so the merge stays a small fraction of the traffic.
+  const int64_t target = bm == 32 ? 8192 : 1024;
+  int64_t splits = base > 0 ? (target + base - 1) / base : 1;
+  const int64_t cap = max_tiles / 4 > 1 ? max_tiles / 4 : 1;
+  if (splits > cap) splits = cap;
+  if (splits > 256) splits = 256;
+  if (splits < 1) splits = 1;
+  int64_t split_tiles = (max_tiles + splits - 1) / splits;
+  splits = (max_tiles + split_tiles - 1) / split_tiles;
+  KvPlan plan;
+  plan.num_splits = (int)splits;
+  plan.split_tiles = (int)split_tiles;
+  const int64_t prow = splits * batch * seqlen_q * heads_q;
+  plan.o_part_bytes = splits > 1 ? ((prow * head_dim * 4 + 255) / 256) * 256 : 0;
+  plan.lse_part_bytes = splits > 1 ? prow * 4 : 0;
+  return plan;
+}
+
+}  // namespace
+
+hipError_t fa_launch_combine(int dtype, const float* o_part, const float* lse_part, void* out,
+                             float* lse, int num_splits, int batch, int seqlen_q, int heads,
+                             int head_dim, const int64_t* o_stride, const int64_t* lse_stride,
+                             hipStream_t st) {
+  const int64_t threads = (int64_t)batch * seqlen_q * heads * (head_dim / 4);
+  const int64_t blocks = (threads + 255) / 256;
+  if (blocks <= 0) return hipSuccess;
+  const int64_t l0 = lse_stride ? lse_stride[0] : 0, l1 = lse_stride ? lse_stride[2] : 0,
+                l2 = lse_stride ? lse_stride[1] : 0;
+  if (dtype == FA_DTYPE_F16)
+    hipLaunchKernelGGL(fa::combine_kernel<fa::F16>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       o_part, lse_part, out, lse, num_splits, batch, seqlen_q, heads, head_dim,
+                       o_stride[0], o_stride[1], o_stride[2], l0, l1, l2);
+  else
+    hipLaunchKernelGGL(fa::combine_kernel<fa::BF16>, dim3((unsigned)blocks), dim3(256), 0, st,
+                       o_part, lse_part, out, lse, num_splits, batch, seqlen_q, heads, head_dim,
+                       o_stride[0], o_stride[1], o_stride[2], l0, l1, l2);
+  return hipGetLastError();
+}
+
+extern "C" {
+
+int fa_version(void) { return 100; }
+
+const char* fa_last_error_string(void) { return g_last_error.c_str(); }
+
+int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* lse,
+                 int64_t batch, int64_t seqlen_q, int64_t seqlen_k, int64_t heads_q,
+                 int64_t heads_k, int64_t head_dim, const int64_t* q_stride,
+                 const int64_t* k_stride, const int64_t* v_stride, const int64_t* o_stride,
+                 const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                 int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
+                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream) {
+  if (!q || !k || !v || !out || !q_stride || !k_stride || !v_stride || !o_stride)
+    return fail(FA_ERR_INVALID, "fa_fwd_dense: null pointer argument");
+  if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_dense: lse without lse_stride");
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: dtype %d not supported", dtype);
+  if (!supported_head_dim(head_dim))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: head_dim %lld not in {16,32,64,128,256}",
+                (long long)head_dim);
+  if (batch < 0 || seqlen_q < 0 || seqlen_k < 0 || heads_q <= 0 || heads_k <= 0 ||
+      heads_q % heads_k != 0)
+    return fail(FA_ERR_INVALID, "fa_fwd_dense: bad sizes B=%lld Sq=%lld Sk=%lld Hq=%lld Hk=%lld",
+                (long long)batch, (long long)seqlen_q, (long long)seqlen_k, (long long)heads_q,
+                (long long)heads_k);
+  if (seqlen_q > INT32_MAX / 2 || seqlen_k > INT32_MAX / 2 || batch * heads_q > INT32_MAX)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: sizes exceed 32-bit indexing");
+  if (!aligned16(q, q_stride, 3) || !aligned16(k, k_stride, 3) || !aligned16(v, v_stride, 3) ||
+      !aligned16(out, o_stride, 3))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: tensors must be 16-byte aligned with strides "
+                                    "that are multiples of 8 elements");
+  if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
+  fa::FwdParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = out; p.lse = lse;
+  p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];
+  p.k_sb = k_stride[0]; p.k_ss = k_stride[1]; p.k_sh = k_stride[2];
+  p.v_sb = v_stride[0]; p.v_ss = v_stride[1]; p.v_sh = v_stride[2];
+  p.o_sb = o_stride[0]; p.o_ss = o_stride[1]; p.o_sh = o_stride[2];
+  if (lse) { p.lse_sb = lse_stride[0]; p.lse_sh = lse_stride[1]; p.lse_ss = lse_stride[2]; }
+  p.batch = (int)batch; p.seqlen_q = (int)seqlen_q; p.seqlen_k = (int)seqlen_k;
+  p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
+  fill_scale(p, softmax_scale, softcap, alibi_slopes);
+  p.alibi_sb = alibi_batch_stride;
+  p.causal = causal != 0;
+  p.window_left = window_left < 0 ? -1 : (int)(window_left > INT32_MAX / 4 ? INT32_MAX / 4 : window_left);
+  p.window_right = window_right < 0 ? -1 : (int)(window_right > INT32_MAX / 4 ? INT32_MAX / 4 : window_right);
+  p.q_offset = q_pos_offset;
+  p.num_splits = 1;
+  p.heavy_first = p.causal || p.window_right >= 0;
+  return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim, needs_generic(p),
+                               (hipStream_t)stream),
+                    "fa_fwd_dense launch");
+}
+
+int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float* lse,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t heads_q, int64_t heads_k,
+                  int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride, const int64_t* lse_stride,
+                  int dtype, float softmax_scale, int causal, int64_t window_left,
+                  int64_t window_right, float softcap, const float* alibi_slopes,
+                  int64_t alibi_batch_stride, fa_stream_t stream) {
+  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k || !q_stride || !k_stride ||
+      !v_stride || !o_stride)
+    return fail(FA_ERR_INVALID, "fa_fwd_varlen: null pointer argument");
+  if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_varlen: lse without lse_stride");
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: dtype %d not supported", dtype);
+  if (!supported_head_dim(head_dim))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: head_dim %lld not in {16,32,64,128,256}",
+                (long long)head_dim);
+  if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || heads_q <= 0 || heads_k <= 0 ||
+      heads_q % heads_k != 0)
+    return fail(FA_ERR_INVALID, "fa_fwd_varlen: bad sizes");
+  if (max_seqlen_q > INT32_MAX / 2 || batch * heads_q > INT32_MAX)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: sizes exceed 32-bit indexing");
+  if (!aligned16(q, q_stride, 2) || !aligned16(k, k_stride, 2) || !aligned16(v, v_stride, 2) ||
+      !aligned16(out, o_stride, 2))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: tensors must be 16-byte aligned with strides "
+                                    "that are multiples of 8 elements");
+  if (batch == 0 || max_seqlen_q == 0) return hip_status(hipSuccess, "");
+  fa::FwdParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = out; p.lse = lse;
+  p.q_ss = q_stride[0]; p.q_sh = q_stride[1];
+  p.k_ss = k_stride[0]; p.k_sh = k_stride[1];
+  p.v_ss = v_stride[0]; p.v_sh = v_stride[1];
+  p.o_ss = o_stride[0]; p.o_sh = o_stride[1];
+  if (lse) { p.lse_ss = lse_stride[0]; p.lse_sh = lse_stride[1]; }
+  p.cu_q = cu_seqlens_q; p.cu_k = cu_seqlens_k;
+  p.batch = (int)batch; p.seqlen_q = (int)max_seqlen_q; p.seqlen_k = (int)max_seqlen_k;
+  p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
+  fill_scale(p, softmax_scale, softcap, alibi_slopes);
+  p.alibi_sb = alibi_batch_stride;
+  p.causal = causal != 0;
+  p.window_left = window_left < 0 ? -1 : (int)(window_left > INT32_MAX / 4 ? INT32_MAX / 4 : window_left);
+  p.window_right = window_right < 0 ? -1 : (int)(window_right > INT32_MAX / 4 ? INT32_MAX / 4 : window_right);
+  p.num_splits = 1;
+  p.heavy_first = p.causal || p.window_right >= 0;
+  return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim, needs_generic(p),
+                               (hipStream_t)stream),
+                    "fa_fwd_varlen launch");
+}
+
+int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
+                        int64_t head_dim, int64_t max_keys, int32_t* num_splits,
+                        int64_t* workspace_bytes) {
+  if (!num_splits || !workspace_bytes)
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache_plan: null output pointer");
+  if (batch < 0 || seqlen_q < 0 || heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0 ||
+      max_keys < 0)
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache_plan: bad sizes");
+  if (!supported_head_dim(head_dim))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache_plan: head_dim %lld not supported",
+                (long long)head_dim);
+  const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys);
+  *num_splits = plan.num_splits;
+  *workspace_bytes = plan.o_part_bytes + plan.lse_part_bytes;
+  g_last_error.clear();
+  return FA_OK;
+}
+
+int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void* out,
+                   float* lse, const int32_t* cache_seqlens, const int32_t* block_table,
+                   int64_t block_table_stride, int64_t page_size, const int32_t* cache_batch_idx,
+                   const int32_t* cache_leftpad, int64_t batch, int64_t seqlen_q,
+                   int64_t max_keys, int64_t heads_q, int64_t heads_k, int64_t head_dim,
+                   const int64_t* q_stride, const int64_t* k_cache_stride,
+                   const int64_t* v_cache_stride, const int64_t* o_stride,
+                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                   int64_t window_left, int64_t window_right, const float* alibi_slopes,
+                   int64_t alibi_batch_stride, int32_t num_splits, void* workspace,
+                   int64_t workspace_bytes, fa_stream_t stream) {
+  if (!q || !k_cache || !v_cache || !out || !q_stride || !k_cache_stride || !v_cache_stride ||
+      !o_stride)
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: null pointer argument");
+  if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_kvcache: lse without lse_stride");
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: dtype %d not supported", dtype);
+  if (!supported_head_dim(head_dim))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: head_dim %lld not supported",
+                (long long)head_dim);
+  if (batch < 0 || seqlen_q < 0 || max_keys < 0 || heads_q <= 0 || heads_k <= 0 ||
+      heads_q % heads_k != 0)
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: bad sizes");
+  if (block_table && page_size <= 0)
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: page_size must be positive");
+  if (seqlen_q * (heads_q / heads_k) > INT32_MAX / 2 || max_keys > INT32_MAX / 2)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: sizes exceed 32-bit indexing");
+  if (!aligned16(q, q_stride, 3) || !aligned16(k_cache, k_cache_stride, 3) ||
+      !aligned16(v_cache, v_cache_stride, 3) || !aligned16(out, o_stride, 3))
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: tensors must be 16-byte aligned with "
+                                    "strides that are multiples of 8 elements");
+  const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys);
+  if (num_splits != plan.num_splits)
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: num_splits %d does not match the plan (%d)",
+                (int)num_splits, plan.num_splits);
+  if (plan.num_splits > 1 &&
+      (!workspace || workspace_bytes < plan.o_part_bytes + plan.lse_part_bytes ||
+       reinterpret_cast<uintptr_t>(workspace) % 16 != 0))
+    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: workspace too small or misaligned (%lld < %lld)",
+                (long long)workspace_bytes, (long long)(plan.o_part_bytes + plan.lse_part_bytes));
+  if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
+  fa::FwdParams p{};
+  p.q = q; p.k = k_cache; p.v = v_cache; p.o = out; p.lse = lse;
+  p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];
+  p.k_sb = k_cache_stride[0]; p.k_ss = k_cache_stride[1]; p.k_sh = k_cache_stride[2];
+  p.v_sb = v_cache_stride[0]; p.v_ss = v_cache_stride[1]; p.v_sh = v_cache_stride[2];
+  p.o_sb = o_stride[0]; p.o_ss = o_stride[1]; p.o_sh = o_stride[2];
+  if (lse) { p.lse_sb = lse_stride[0]; p.lse_sh = lse_stride[1]; p.lse_ss = lse_stride[2]; }
+  p.batch = (int)batch; p.seqlen_q = (int)seqlen_q; p.seqlen_k = (int)max_keys;
+  p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
+  fill_scale(p, softmax_scale, 0.f, alibi_slopes);
+  p.alibi_sb = alibi_batch_stride;
+  p.causal = causal != 0;
+  p.kv_causal_offset = causal != 0;
+  p.window_left = window_left < 0 ? -1 : (int)(window_left > INT32_MAX / 4 ? INT32_MAX / 4 : window_left);
+  p.window_right = window_right < 0 ? -1 : (int)(window_right > INT32_MAX / 4 ? INT32_MAX / 4 : window_right);
+  p.seqlens_k = cache_seqlens;
+  p.block_table = block_table; p.bt_stride = block_table_stride; p.page_size = (int)page_size;
+  p.cache_rows = cache_batch_idx; p.leftpad = cache_leftpad;
+  p.num_splits = plan.num_splits; p.split_tiles = plan.split_tiles;
+  if (plan.num_splits > 1) {
+    p.o_part = static_cast<float*>(workspace);
+    p.lse_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.o_part_bytes);
+  }
+  p.heavy_first = 0;
+  hipError_t e = launch_fwd(dtype, p, fa::kModeKvcache, (int)head_dim, needs_generic(p),
+                            (hipStream_t)stream);
+  if (e == hipSuccess && plan.num_splits > 1)
+    e = fa_launch_combine(dtype, p.o_part, p.lse_part, out, lse, plan.num_splits, (int)batch,
+                          (int)seqlen_q, (int)heads_q, (int)head_dim, o_stride, lse_stride,
+                          (hipStream_t)stream);
+  return hip_status(e, "fa_fwd_kvcache launch");
+}
+
+int fa_quant_k_int8(const void* k, int8_t* k8, float* s_k, int64_t batch, int64_t heads,
+                    int64_t seqlen, int64_t head_dim, const int64_t* k_stride,
+                    fa_stream_t stream) {
+  if (!k || !k8 || !s_k || !k_stride) return fail(FA_ERR_INVALID, "fa_quant_k_int8: null pointer");
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(FA_ERR_UNSUPPORTED, "fa_quant_k_int8: head_dim %lld not in {32,64,128,256}",
+                (long long)head_dim);
+  if (batch < 0 || heads <= 0 || seqlen < 0 || batch * heads * seqlen > INT32_MAX)
+    return fail(FA_ERR_INVALID, "fa_quant_k_int8: bad sizes");
+  if (!aligned16(k, k_stride, 3) || reinterpret_cast<uintptr_t>(k8) % 8 != 0 ||
+      reinterpret_cast<uintptr_t>(s_k) % 4 != 0)
+    return fail(FA_ERR_UNSUPPORTED, "fa_quant_k_int8: misaligned tensors");
+  return hip_status(fa_launch_quant_k_int8(k, k8, s_k, (int)batch, (int)heads, (int)seqlen,
+                                           (int)head_dim, k_stride, (hipStream_t)stream),
+                    "fa_quant_k_int8 launch");
+}
+
+int fa_fwd_int8(const void* q, const int8_t* k8, const float* s_k, const void* v, void* out,
+                float* lse, int64_t batch, int64_t heads, int64_t seqlen, int64_t head_dim,
+                const int64_t* q_stride, const int64_t* v_stride, const int64_t* o_stride,
+                float sm_scale, int causal, int64_t seq_len_k, int64_t seq_len_q,
+                fa_stream_t stream) {
+  if (!q || !k8 || !s_k || !v || !out || !q_stride || !v_stride || !o_stride)
+    return fail(FA_ERR_INVALID, "fa_fwd_int8: null pointer argument");
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_int8: head_dim %lld not in {32,64,128,256}",
+                (long long)head_dim);
+  if (batch < 0 || heads <= 0 || seqlen < 0 || batch * heads > INT32_MAX || seqlen > INT32_MAX / 2)
+    return fail(FA_ERR_INVALID, "fa_fwd_int8: bad sizes");
+  if (!aligned16(q, q_stride, 3) || !aligned16(v, v_stride, 3) || !aligned16(out, o_stride, 3) ||
+      reinterpret_cast<uintptr_t>(k8) % 16 != 0)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_int8: misaligned tensors");
+  if (batch == 0 || seqlen == 0) return hip_status(hipSuccess, "");
+  return hip_status(fa_launch_int8_fwd(q, k8, s_k, v, out, lse, (int)batch, (int)heads,
+                                       (int)seqlen, (int)head_dim, q_stride, v_stride, o_stride,
+                                       sm_scale, causal, (int)seq_len_k, (int)seq_len_q,
+                                       (hipStream_t)stream),
+                    "fa_fwd_int8 launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,88 @@
+// Shared device-side types and helpers for the gfx950 (CDNA4) attention kernels.
+//
+// Everything here targets one architecture: 64-wide wavefronts, the CDNA4
+// matrix cores (v_mfma_f32_32x32x16_{f16,bf16}, v_mfma_i32_32x32x32_i8) and
+// v_permlane32_swap for exchanging values between the two 32-lane halves of a
+// wave.  There is no portability layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fa {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Element-type tags.  Storage is handled as raw 16-bit words; the MFMA and
+// conversion wrappers reinterpret them.
+struct F16 {
+  static constexpr int kBytes = 2;
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  // Round-to-nearest-even pack of two floats (v_cvt_pk_f16_f32).
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    f32x2 x = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2));
+  }
+  __device__ static inline float to_float(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+};
+
+struct BF16 {
+  static constexpr int kBytes = 2;
+  __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  // Round-to-nearest-even pack of two floats (v_cvt_pk_bf16_f32).
+  __device__ static inline uint32_t pack2(float lo, float hi) {
+    f32x2 x = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2));
+  }
+  __device__ static inline float to_float(uint16_t h) {
+    return __builtin_bit_cast(float, (uint32_t)h << 16);
+  }
+};
+
+// Exchange a value between lane l and lane l^32 and combine both copies:
+// v_permlane32_swap moves the upper half of `a` and the lower half of `b`;
+// with a == b == x the two results hold x[l % 32] and x[l % 32 + 32].
+__device__ inline float halves_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ inline float halves_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// blockIdx.x -> logical work id so that consecutive logical ids run on the
+// same XCD.  Hardware dispatches workgroup L to XCD L % 8; grouping the work
+// of one (batch, head) on one XCD keeps its K/V tiles in that XCD's L2.
+__device__ inline int xcd_remap(int L, int total) {
+  constexpr int kXcds = 8;
+  const int per = total / kXcds;
+  if (L >= per * kXcds) return L;
+  return (L % kXcds) * per + L / kXcds;
+}
+
+__device__ inline u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ inline void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+}  // namespace fa

@@ -1,0 +1,99 @@
+// Host-side launch helpers for fwd_kernel: tile choice per head dim and the
+// grid decomposition.  Instantiated once per element type (fa_fwd_f16.hip,
+// fa_fwd_bf16.hip) so the two halves compile in parallel.
+#pragma once
+
+#include "fa_fwd_kernel.h"
+
+namespace fa {
+
+// Tile shape per head dim (prefill): 4 waves x 32 rows; 64-key tiles except
+// D=256, where 32-key tiles keep the double-buffered K/V^T tiles and the
+// 128-register O accumulator within budget.
+template <int D> struct PrefillCfg { static constexpr int NW = 4, BN = D >= 256 ? 32 : 64; };
+// KV-cache: one wave owns up to 32 (query, head-in-group) rows; more rows use
+// four waves.  32-key tiles keep the single wave's prefetch registers small.
+template <int D> struct KvCfg1 { static constexpr int NW = 1, BN = 32; };
+template <int D> struct KvCfg4 { static constexpr int NW = 4, BN = D >= 256 ? 32 : 64; };
+
+template <class T, int D, int NW, int BN, int MODE, bool GEN>
+hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipStream_t st) {
+  using Tile = FwdTile<D, NW, BN>;
+  auto kern = fwd_kernel<T, D, NW, BN, MODE, GEN>;
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    lds_attr_set = true;
+  }
+  p.n_mblocks = (rows_for_grid + Tile::BM - 1) / Tile::BM;
+  const int64_t total = (int64_t)p.n_mblocks * outer_blocks;
+  if (total <= 0) return hipSuccess;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+  p.total_blocks = (int)total;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  return hipGetLastError();
+}
+
+template <class T, int D, int MODE, bool GEN>
+hipError_t launch_fwd_d(const FwdParams& p, hipStream_t st) {
+  if (MODE == kModePrefill) {
+    using C = PrefillCfg<D>;
+    return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, p.seqlen_q, p.heads_q * p.batch, st);
+  }
+  const int rows = p.seqlen_q * p.group;
+  const int outer = p.heads_k * p.batch * p.num_splits;
+  if (rows <= 32 && D <= 128) {
+    using C = KvCfg1<D>;
+    return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, rows, outer, st);
+  }
+  using C = KvCfg4<D>;
+  return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, rows, outer, st);
+}
+
+template <class T, int MODE>
+hipError_t launch_fwd_mode(const FwdParams& p, int head_dim, bool generic, hipStream_t st) {
+#define FA_CASE(DD)                                                         \
+  case DD:                                                                  \
+    return generic ? launch_fwd_d<T, DD, MODE, true>(p, st)                 \
+                   : launch_fwd_d<T, DD, MODE, false>(p, st);
+  switch (head_dim) {
+    FA_CASE(16)
+    FA_CASE(32)
+    FA_CASE(64)
+    FA_CASE(128)
+    FA_CASE(256)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef FA_CASE
+}
+
+// Key-tile width the KV-cache launch will use (needed to size split-KV work).
+inline int kvcache_tile_keys(int rows, int head_dim) {
+  if (rows <= 32 && head_dim <= 128) return 32;
+  return head_dim >= 256 ? 32 : 64;
+}
+
+}  // namespace fa
+
+// Launch entry points shared by the C ABI (fa_api.hip): forward kernels are
+// defined per element type in fa_fwd_f16.hip / fa_fwd_bf16.hip, the INT8 path
+// in fa_int8.hip and the split-KV merge in fa_api.hip.
+hipError_t fa_launch_fwd_f16(const fa::FwdParams& p, int mode, int head_dim, bool generic,
+                             hipStream_t st);
+hipError_t fa_launch_fwd_bf16(const fa::FwdParams& p, int mode, int head_dim, bool generic,
+                              hipStream_t st);
+hipError_t fa_launch_combine(int dtype, const float* o_part, const float* lse_part, void* out,
+                             float* lse, int num_splits, int batch, int seqlen_q, int heads,
+                             int head_dim, const int64_t* o_stride, const int64_t* lse_stride,
+                             hipStream_t st);
+hipError_t fa_launch_quant_k_int8(const void* k, int8_t* k8, float* s_k, int batch, int heads,
+                                  int seqlen, int head_dim, const int64_t* k_stride,
+                                  hipStream_t st);
+hipError_t fa_launch_int8_fwd(const void* q, const int8_t* k8, const float* s_k, const void* v,
+                              void* o, float* lse, int batch, int heads, int seqlen, int head_dim,
+                              const int64_t* q_stride, const int64_t* v_stride,
+                              const int64_t* o_stride, float sm_scale, int causal, int seq_len_k,
+                              int seq_len_q, hipStream_t st);

@@ -1,0 +1,204 @@
+"""ctypes binding of ``libfa_gfx950.so`` (C ABI: ``include/fa_gfx950.h``).
+
+The library is built in tree by ``build_native.py`` (``__graft_entry__.build()``
+runs it) into ``flash_attn_triton/_lib/``.  There is no fallback: if the
+library is missing or cannot be loaded every attention entry point raises.
+
+Each wrapper takes torch tensors, passes raw device pointers, element strides
+and ``torch.cuda.current_stream()``'s handle, and turns a nonzero status into
+``RuntimeError`` carrying ``fa_last_error_string()``.  Launches are
+asynchronous on the current stream, as the reference's Triton launches are.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+from typing import Optional, Sequence
+
+import torch
+
+_LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libfa_gfx950.so"
+
+FA_OK = 0
+FA_ERR_INVALID = 1
+FA_ERR_UNSUPPORTED = 2
+FA_ERR_HIP = 3
+FA_DTYPE_F16 = 0
+FA_DTYPE_BF16 = 1
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_int = ctypes.c_int
+_f32 = ctypes.c_float
+_vp = ctypes.c_void_p
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+
+# name -> (restype, argtypes); mirrors include/fa_gfx950.h
+_SIGNATURES = {
+    "fa_version": (_int, []),
+    "fa_last_error_string": (ctypes.c_char_p, []),
+    "fa_fwd_dense": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
+                            _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64,
+                            _i64, _f32, _vp, _i64, _vp]),
+    "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                             _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
+                             _i64, _f32, _vp, _i64, _vp]),
+    "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
+    "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
+                              _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
+                              _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp]),
+    "fa_quant_k_int8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _vp]),
+    "fa_fwd_int8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p,
+                           _i64p, _f32, _int, _i64, _i64, _vp]),
+}
+
+_lock = threading.Lock()
+_lib: Optional[ctypes.CDLL] = None
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library once; raise ``RuntimeError`` if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not _LIB_PATH.exists():
+            raise RuntimeError(
+                f"flash_attn_triton: HIP library not found at {_LIB_PATH}; build it with "
+                "`python flash-attn-triton_amd/build_native.py` (or __graft_entry__.build())")
+        lib = ctypes.CDLL(os.fspath(_LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def _check(status: int, what: str) -> None:
+    if status != FA_OK:
+        msg = load().fa_last_error_string()
+        msg = msg.decode() if msg else ""
+        raise RuntimeError(f"{what} failed (status {status}): {msg}")
+
+
+def _strides(values: Sequence[int]):
+    return (ctypes.c_int64 * len(values))(*[int(v) for v in values])
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float16:
+        return FA_DTYPE_F16
+    if dtype == torch.bfloat16:
+        return FA_DTYPE_BF16
+    raise RuntimeError(f"flash_attn_triton: the HIP kernels take fp16 or bf16, not {dtype}")
+
+
+def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offset: int,
+              window_left: int, window_right: int, softcap: float, alibi) -> None:
+    """q [B,Sq,Hq,D], k/v [B,Sk,Hk,D] (BSHD strides), out like q; lse [B,Hq,Sq] or None."""
+    lib = load()
+    B, Sq, Hq, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    lse_stride = _strides(lse.stride()) if lse is not None else None
+    status = lib.fa_fwd_dense(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), B, Sq, Sk, Hq, Hk, D,
+        _strides(q.stride()[:3]), _strides(k.stride()[:3]), _strides(v.stride()[:3]),
+        _strides(out.stride()[:3]), lse_stride, dtype_code(q.dtype), float(softmax_scale),
+        int(bool(causal)), int(q_pos_offset), int(window_left), int(window_right), float(softcap),
+        _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)), _stream(q.device))
+    _check(status, "fa_fwd_dense")
+
+
+def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
+               softmax_scale: float, causal: bool, window_left: int, window_right: int,
+               softcap: float, alibi) -> None:
+    """q [Tq,Hq,D], k/v [Tk,Hk,D]; cu_* int32 [batch+1]; lse [Tq,Hq] or None."""
+    lib = load()
+    Hq, D = q.shape[1], q.shape[2]
+    Hk = k.shape[1]
+    batch = cu_q.numel() - 1
+    lse_stride = _strides(lse.stride()) if lse is not None else None
+    status = lib.fa_fwd_varlen(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), _ptr(cu_q), _ptr(cu_k), batch,
+        int(max_seqlen_q), int(max_seqlen_k), Hq, Hk, D, _strides(q.stride()[:2]),
+        _strides(k.stride()[:2]), _strides(v.stride()[:2]), _strides(out.stride()[:2]),
+        lse_stride, dtype_code(q.dtype), float(softmax_scale), int(bool(causal)),
+        int(window_left), int(window_right), float(softcap), _ptr(alibi),
+        0 if alibi is None else int(alibi.stride(0)), _stream(q.device))
+    _check(status, "fa_fwd_varlen")
+
+
+def kvcache_plan(batch: int, seqlen_q: int, heads_q: int, heads_k: int, head_dim: int,
+                 max_keys: int):
+    lib = load()
+    splits = ctypes.c_int32(0)
+    ws = ctypes.c_int64(0)
+    _check(lib.fa_fwd_kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
+                                   ctypes.byref(splits), ctypes.byref(ws)),
+           "fa_fwd_kvcache_plan")
+    return int(splits.value), int(ws.value)
+
+
+def fwd_kvcache(q, k_cache, v_cache, out, lse, cache_seqlens, block_table, cache_batch_idx,
+                cache_leftpad, max_keys: int, softmax_scale: float, causal: bool,
+                window_left: int, window_right: int, alibi, workspace=None) -> None:
+    """Attention of q [B,Sq,Hq,D] against a paged or batched cache (see fa_fwd_kvcache)."""
+    lib = load()
+    B, Sq, Hq, D = q.shape
+    Hk = k_cache.shape[2]
+    splits, ws_bytes = kvcache_plan(B, Sq, Hq, Hk, D, max_keys)
+    if ws_bytes > 0 and (workspace is None or workspace.numel() < ws_bytes):
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    page_size = k_cache.shape[1] if block_table is not None else 0
+    bt_stride = block_table.stride(0) if block_table is not None else 0
+    lse_stride = _strides(lse.stride()) if lse is not None else None
+    status = lib.fa_fwd_kvcache(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(lse), _ptr(cache_seqlens),
+        _ptr(block_table), int(bt_stride), int(page_size), _ptr(cache_batch_idx),
+        _ptr(cache_leftpad), B, Sq, int(max_keys), Hq, Hk, D, _strides(q.stride()[:3]),
+        _strides(k_cache.stride()[:3]), _strides(v_cache.stride()[:3]),
+        _strides(out.stride()[:3]), lse_stride, dtype_code(q.dtype), float(softmax_scale),
+        int(bool(causal)), int(window_left), int(window_right), _ptr(alibi),
+        0 if alibi is None else int(alibi.stride(0)), splits, _ptr(workspace),
+        int(ws_bytes), _stream(q.device))
+    _check(status, "fa_fwd_kvcache")
+
+
+def quant_k_int8(k, k8, s_k) -> None:
+    """k [B,H,S,D] fp16 -> k8 [B*H,S,D] int8, s_k [B*H,S] fp32."""
+    lib = load()
+    B, H, S, D = k.shape
+    st = k.stride()
+    status = lib.fa_quant_k_int8(_ptr(k), _ptr(k8), _ptr(s_k), B, H, S, D,
+                                 _strides((st[0], st[1], st[2])), _stream(k.device))
+    _check(status, "fa_quant_k_int8")
+
+
+def fwd_int8(q, k8, s_k, v, out, lse, sm_scale: float, causal: bool, seq_len_k: int,
+             seq_len_q: int) -> None:
+    """q/v/out [B,H,S,D] fp16 with {batch, head, seq} strides; lse [B,H,S] or None."""
+    lib = load()
+    B, H, S, D = q.shape
+    status = lib.fa_fwd_int8(
+        _ptr(q), _ptr(k8), _ptr(s_k), _ptr(v), _ptr(out), _ptr(lse), B, H, S, D,
+        _strides(q.stride()[:3]), _strides(v.stride()[:3]), _strides(out.stride()[:3]),
+        float(sm_scale), int(bool(causal)), int(seq_len_k), int(seq_len_q), _stream(q.device))
+    _check(status, "fa_fwd_int8")

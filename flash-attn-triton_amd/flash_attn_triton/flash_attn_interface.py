@@ -1,0 +1,553 @@
+"""Public FlashAttention-2 style API of the gfx950 build.
+
+Same names, signatures, defaults, validation order and messages as the
+reference's ``flash_attn_triton/flash_attn_interface.py`` (cited per
+function), so existing call sites keep working.  Every attention result is
+computed by the HIP kernels in ``libfa_gfx950.so``; there is no Triton and no
+host-side fallback.
+
+Deliberate differences from the reference (each one removes a reference
+defect or a host-side copy, never changes a correct result):
+
+* inputs are not padded to multiples of 64, grouped KV heads are never
+  repeated, strided inputs are read in place: the kernels handle ragged
+  lengths, GQA and BSHD strides directly;
+* bf16 inputs are accepted (the reference takes fp16/fp32 only);
+* ``flash_attn_with_kvcache`` runs one batched split-KV launch instead of a
+  Python loop of gathers and O(L^2) padded launches, and its causal
+  alignment is bottom-right for every cache length (the reference's dense
+  stage split drops keys past the first tile when ``L > BLOCK_M``);
+* only the forward pass exists: ``backward`` raises ``NotImplementedError``,
+  and ``dropout_p > 0`` is rejected.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from .triton_kernel.attention_kernel import (
+    DROPOUT_MSG,
+    _wrap_grad,
+    attention,
+    attention_varlen,
+    dense_forward,
+    varlen_forward,
+)
+from . import _native
+
+BLOCK_SIZE = 64
+
+_FP32_MSG = (
+    "flash_attn_triton (gfx950 HIP build): fp32 inputs are not implemented by the HIP "
+    "kernels yet; pass fp16 or bf16 tensors")
+
+
+def _check_compute_dtype(dtype):
+    if dtype == torch.float32:
+        raise NotImplementedError(_FP32_MSG)
+
+
+def _normalize_alibi(alibi_slopes, batch, heads, device):
+    """(H,) or (B,H) fp32 slopes -> contiguous (B,H) (flash_attn_interface.py:128-136)."""
+    if alibi_slopes is None:
+        return None
+    alibi_slopes = torch.as_tensor(alibi_slopes, device=device, dtype=torch.float32)
+    if alibi_slopes.ndim == 1:
+        if alibi_slopes.shape[0] != heads:
+            raise ValueError("alibi_slopes must have one value per query head")
+        alibi_slopes = alibi_slopes.unsqueeze(0).expand(batch, -1)
+    elif alibi_slopes.shape != (batch, heads):
+        raise ValueError("alibi_slopes must have shape (nheads,) or (batch, nheads)")
+    return alibi_slopes.contiguous()
+
+
+def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
+                          alibi_slopes, attn_bias=None, causal_offset=0):
+    """Materialized-probabilities path (``return_attn_probs`` / ``attn_bias``).
+
+    The reference computes this option with dense torch math
+    (flash_attn_interface.py:15-49); it is not built in this HIP-only port yet.
+    """
+    raise NotImplementedError(
+        "flash_attn_triton (gfx950 HIP build): return_attn_probs=True and attn_bias are not "
+        "implemented by the HIP kernels yet")
+
+
+def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
+                    window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                    deterministic=False, return_attn_probs=False, use_native_gqa=False,
+                    attn_bias=None):
+    """Flash attention forward (reference flash_attn_interface.py:68-246).
+
+    Arguments:
+        q: (batch_size, seqlen, nheads, headdim)
+        k: (batch_size, seqlen, nheads_k, headdim)
+        v: (batch_size, seqlen, nheads_k, headdim)
+        dropout_p: float. Dropout probability (only 0.0 is built).
+        softmax_scale: float. Default 1 / sqrt(headdim).
+        causal: bool. Upper-left aligned causal mask.
+        window_size: (left, right). Sliding window, -1 = unbounded.
+        softcap: float. softcap * tanh(score / softcap) when > 0.
+        alibi_slopes: (nheads,) or (batch_size, nheads) fp32; subtracted as
+            slope * |i - j| before softcap.
+        deterministic, use_native_gqa: accepted for compatibility; the forward
+            kernel is deterministic and always reads grouped KV heads natively.
+    Return:
+        out: (batch_size, seqlen, nheads, headdim).
+    """
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError("This implementation supports FP16, BF16 and FP32 tensors")
+    if softcap < 0.0:
+        raise ValueError("softcap must be non-negative")
+    if dropout_p < 0.0 or dropout_p >= 1.0:
+        raise ValueError("dropout_p must be in the range [0, 1)")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("All attention tensors must be CUDA tensors")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have shape (batch, seqlen, heads, headdim)")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k, and v must have the same dtype")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k, and v must be on the same CUDA device")
+
+    batch_size, seq_len_q, n_heads_q, head_dim = q.shape
+    key_batch_size, seq_len_k, n_heads_k, key_head_dim = k.shape
+    value_batch_size, value_seq_len, value_heads, value_head_dim = v.shape
+    if key_batch_size != batch_size or value_batch_size != batch_size:
+        raise ValueError("q, k, and v must have the same batch size")
+    if value_seq_len != seq_len_k:
+        raise ValueError("k and v must have the same sequence length")
+    if key_head_dim != head_dim or value_head_dim != head_dim:
+        raise ValueError("q, k, and v must have the same head dimension")
+    if value_heads != n_heads_k:
+        raise ValueError("k and v must have the same number of heads")
+    if n_heads_k == 0 or n_heads_q % n_heads_k != 0:
+        raise ValueError(
+            f"Number of heads in Q ({n_heads_q}) must be divisible by number of heads in K/V ({n_heads_k})"
+        )
+    alibi_slopes = _normalize_alibi(alibi_slopes, batch_size, n_heads_q, q.device)
+    use_alibi = alibi_slopes is not None and bool(torch.any(alibi_slopes != 0))
+
+    if return_attn_probs:
+        return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
+                                     softcap, alibi_slopes, attn_bias)
+    if attn_bias is not None:
+        return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
+                                     softcap, alibi_slopes, attn_bias)[0]
+
+    if seq_len_q != seq_len_k:
+        return flash_attn_func_cross(
+            q, k, v, dropout_p=dropout_p, softmax_scale=softmax_scale,
+            causal=causal, use_native_gqa=use_native_gqa, softcap=softcap,
+            alibi_slopes=alibi_slopes, window_size=window_size,
+            deterministic=deterministic,
+        )
+    # Equal-length path: unsupported head dims surface as AssertionError, as in
+    # the reference's _launch_dense_forward (attention_kernel.py:1063-1064).
+    assert head_dim in {16, 32, 64, 128, 256}
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    _check_compute_dtype(q.dtype)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(head_dim)
+    out = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                        window_left=window_size[0], window_right=window_size[1],
+                        softcap=softcap, alibi=alibi_slopes if use_alibi else None)
+    return _wrap_grad(out, q, k, v)
+
+
+def flash_attn_func_cross(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
+                          use_native_gqa=False, softcap=0.0, alibi_slopes=None,
+                          window_size=(-1, -1), deterministic=False,
+                          return_attn_probs=False, attn_bias=None, _causal_offset=0):
+    """Cross attention for unequal query and KV lengths (reference :249-330).
+
+    Query row ``i`` sits at position ``i + _causal_offset`` (0: upper-left,
+    the SDPA convention for rectangular masks).
+    """
+    if (q.dtype not in (torch.float16, torch.bfloat16, torch.float32) or k.dtype != q.dtype
+            or v.dtype != q.dtype):
+        raise ValueError("flash_attn_func_cross supports matching FP16, BF16 or FP32 tensors")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("All attention tensors must be CUDA tensors")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, and v must have shape (batch, seqlen, heads, headdim)")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k, and v must be on the same CUDA device")
+    if k.shape[0] != q.shape[0] or v.shape[:2] != k.shape[:2]:
+        raise ValueError("q, k, and v have incompatible batch or sequence dimensions")
+    if q.shape[-1] != k.shape[-1] or k.shape[-1] != v.shape[-1]:
+        raise ValueError("q, k, and v must have the same head dimension")
+    if q.shape[-1] not in (16, 32, 64, 128, 256):
+        raise ValueError("head dimension must be one of 16, 32, 64, 128, or 256")
+    if q.shape[2] % k.shape[2] != 0:
+        raise ValueError("The number of query heads must be divisible by KV heads")
+    if dropout_p < 0.0 or dropout_p >= 1.0:
+        raise ValueError("dropout_p must be in the range [0, 1)")
+    if softcap < 0.0:
+        raise ValueError("softcap must be non-negative")
+    if v.shape[2] != k.shape[2]:
+        raise ValueError("k and v must have the same number of heads")
+
+    q_heads = q.shape[2]
+    alibi_slopes = _normalize_alibi(alibi_slopes, q.shape[0], q_heads, q.device)
+    use_alibi = alibi_slopes is not None and bool(torch.any(alibi_slopes != 0))
+
+    if return_attn_probs:
+        return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
+                                     softcap, alibi_slopes, attn_bias,
+                                     causal_offset=_causal_offset)
+    if attn_bias is not None:
+        return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
+                                     softcap, alibi_slopes, attn_bias,
+                                     causal_offset=_causal_offset)[0]
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    _check_compute_dtype(q.dtype)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    out = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                        q_pos_offset=_causal_offset, window_left=window_size[0],
+                        window_right=window_size[1], softcap=softcap,
+                        alibi=alibi_slopes if use_alibi else None)
+    return _wrap_grad(out, q, k, v)
+
+
+def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=False,
+                              window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                              deterministic=False, return_attn_probs=False,
+                              use_native_gqa=False, attn_bias=None):
+    """Packed QKV (reference :337-371). qkv: (batch_size, seqlen, 3, nheads, headdim).
+
+    The three strided slices are read in place (token stride 3*H*D); the
+    reference copies each slice to a contiguous tensor first.
+    """
+    qkv = qkv.contiguous() if not qkv.is_contiguous() else qkv
+    q, k, v = qkv.unbind(dim=2)
+    return flash_attn_func(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
+                           alibi_slopes, deterministic, return_attn_probs, use_native_gqa,
+                           attn_bias)
+
+
+def flash_attn_kvpacked_func(q, kv, dropout_p=0.0, softmax_scale=None, causal=False,
+                             window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                             deterministic=False, return_attn_probs=False,
+                             use_native_gqa=False, attn_bias=None):
+    """Packed KV (reference :374-406). kv: (batch_size, seqlen_k, 2, nheads_k, headdim)."""
+    kv = kv.contiguous() if not kv.is_contiguous() else kv
+    k, v = kv.unbind(dim=2)
+    return flash_attn_func(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
+                           alibi_slopes, deterministic, return_attn_probs, use_native_gqa,
+                           attn_bias)
+
+
+def flash_attn_with_kvcache(
+    q,
+    k_cache,
+    v_cache,
+    k=None,
+    v=None,
+    rotary_cos=None,
+    rotary_sin=None,
+    cache_seqlens=None,
+    cache_batch_idx=None,
+    cache_leftpad=None,
+    block_table=None,
+    softmax_scale=None,
+    causal=False,
+    window_size=(-1, -1),
+    rotary_interleaved=True,
+    alibi_slopes=None,
+):
+    """Attention against a (paged or batched) KV cache (reference :409-525).
+
+    q: (batch, seqlen_q, nheads, headdim).  Paged: k_cache/v_cache
+    (num_pages, page_size, nheads_k, headdim) with block_table
+    (batch, max_num_pages) int32; batched: (batch_cache, seqlen_cache,
+    nheads_k, headdim).  cache_seqlens: visible keys per batch item.  With
+    ``causal`` query i sits at position ``i + L - seqlen_q`` (bottom-right).
+    Returns (batch, seqlen_q, nheads, headdim).
+    """
+    paged = block_table is not None
+    if (rotary_cos is None) != (rotary_sin is None):
+        raise ValueError("rotary_cos and rotary_sin must be supplied together")
+    if q.ndim != 4 or k_cache.ndim != 4 or v_cache.ndim != 4:
+        raise ValueError("q and KV caches must be rank-4 tensors")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must have the same shape")
+    if paged:
+        if block_table.ndim != 2 or block_table.shape[0] != q.shape[0]:
+            raise ValueError("block_table must have shape (batch, max_num_pages)")
+        if block_table.dtype not in (torch.int32, torch.int64):
+            raise ValueError("block_table must contain integer page indices")
+        if torch.any(block_table < 0) or torch.any(block_table >= k_cache.shape[0]):
+            raise ValueError("block_table contains an invalid physical page index")
+        if cache_leftpad is not None:
+            raise ValueError("cache_leftpad cannot be combined with paged KV caches")
+        page_size = k_cache.shape[1]
+        cache_capacity = block_table.shape[1] * page_size
+    else:
+        cache_capacity = k_cache.shape[1]
+    if q.shape[-1] != k_cache.shape[-1]:
+        raise ValueError("q and KV cache dimensions are incompatible")
+    if q.device != k_cache.device or q.device != v_cache.device:
+        raise ValueError("q and KV caches must be on the same device")
+    if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
+        raise ValueError("q and KV caches must have the same dtype")
+    if paged and cache_batch_idx is not None:
+        raise ValueError("cache_batch_idx cannot be combined with paged KV caches")
+    if cache_batch_idx is None:
+        cache_rows = None
+    else:
+        cache_rows = torch.as_tensor(cache_batch_idx, device=q.device, dtype=torch.long).flatten()
+        if (cache_rows.numel() != q.shape[0] or torch.any(cache_rows < 0)
+                or torch.any(cache_rows >= k_cache.shape[0])):
+            raise ValueError("cache_batch_idx must contain valid cache-row indices")
+    if cache_leftpad is None:
+        leftpads = None
+    else:
+        leftpads = torch.as_tensor(cache_leftpad, device=q.device, dtype=torch.long).flatten()
+        if leftpads.numel() != q.shape[0] or torch.any(leftpads < 0):
+            raise ValueError("cache_leftpad must contain one non-negative value per query batch")
+    zero_pad = 0 if leftpads is None else leftpads
+    if k is not None or v is not None:
+        raise NotImplementedError(
+            "flash_attn_triton (gfx950 HIP build): appending k/v to the cache is not "
+            "implemented yet")
+    if rotary_cos is not None:
+        raise NotImplementedError(
+            "flash_attn_triton (gfx950 HIP build): rotary embedding in "
+            "flash_attn_with_kvcache is not implemented yet")
+    if cache_seqlens is None:
+        lengths = torch.full((q.shape[0],), cache_capacity, dtype=torch.int64, device=q.device)
+    else:
+        lengths = torch.as_tensor(cache_seqlens, device=q.device, dtype=torch.int64).flatten()
+    if (lengths.numel() != q.shape[0] or torch.any(lengths < 0)
+            or torch.any(lengths + zero_pad > cache_capacity)):
+        raise ValueError("cache_seqlens must contain valid lengths for every batch item")
+    if q.shape[-1] not in (16, 32, 64, 128, 256):
+        raise ValueError("head dimension must be one of 16, 32, 64, 128, or 256")
+    if q.shape[2] % k_cache.shape[2] != 0:
+        raise ValueError("The number of query heads must be divisible by KV heads")
+    _check_compute_dtype(q.dtype)
+    if q.shape[0] == 0:
+        return q.new_empty(q.shape)
+    alibi = _normalize_alibi(alibi_slopes, q.shape[0], q.shape[2], q.device)
+    if alibi is not None and not bool(torch.any(alibi != 0)):
+        alibi = None
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    from .triton_kernel.attention_kernel import _kernel_ready
+    qk = _kernel_ready(q)
+    kc, vc = _kernel_ready(k_cache), _kernel_ready(v_cache)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    _native.fwd_kvcache(
+        qk, kc, vc, out, None, lengths.to(torch.int32).contiguous(),
+        block_table.to(torch.int32).contiguous() if paged else None,
+        cache_rows.to(torch.int32).contiguous() if cache_rows is not None else None,
+        leftpads.to(torch.int32).contiguous() if leftpads is not None else None,
+        int(cache_capacity), softmax_scale, causal, window_size[0], window_size[1], alibi)
+    return _wrap_grad(out, q)
+
+
+def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                           max_seqlen_k, dropout_p=0.0, softmax_scale=None, causal=False,
+                           window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
+                           deterministic=False, return_attn_probs=False, block_table=None,
+                           seqused_q=None, seqused_k=None, **kwargs):
+    """Packed variable-length attention (reference :527-690).
+
+    q: (total_q, nheads, headdim), k/v: (total_k, nheads_k, headdim),
+    cu_seqlens_*: (batch + 1,) int32 prefix sums.  Returns (total_q, nheads, headdim).
+    """
+    if block_table is not None:
+        if k.ndim != 4 or v.ndim != 4 or k.shape != v.shape:
+            raise ValueError("paged varlen k and v must have shape (pages, page_size, heads, dim)")
+        if block_table.ndim != 2 or block_table.shape[0] != cu_seqlens_k.numel() - 1:
+            raise ValueError("block_table must have shape (batch, max_num_pages)")
+        page_size = k.shape[1]
+        lengths_k = (cu_seqlens_k[1:] - cu_seqlens_k[:-1]).to(torch.long)
+        page_counts = (lengths_k + page_size - 1) // page_size
+        cols = torch.arange(block_table.shape[1], device=block_table.device)
+        used = cols[None, :] < page_counts[:, None].to(block_table.device)
+        used_ids = block_table[used].to(torch.long)
+        if torch.any(used_ids < 0) or torch.any(used_ids >= k.shape[0]):
+            raise ValueError("block_table contains an invalid physical page index")
+        raise NotImplementedError(
+            "flash_attn_triton (gfx950 HIP build): paged varlen prefill "
+            "(block_table in flash_attn_varlen_func) is not implemented yet")
+    batch_size = cu_seqlens_q.numel() - 1
+    if seqused_q is not None or seqused_k is not None:
+        raise NotImplementedError(
+            "flash_attn_triton (gfx950 HIP build): seqused_q / seqused_k are not implemented yet")
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
+        raise ValueError("packed q, k, and v must be rank-3 tensors with matching KV shapes")
+    if cu_seqlens_q.ndim != 1 or cu_seqlens_k.ndim != 1:
+        raise ValueError("cu_seqlens arrays must be one-dimensional")
+    if cu_seqlens_q.numel() != cu_seqlens_k.numel():
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same batch size")
+    if cu_seqlens_q.numel() == 0 or cu_seqlens_q[0].item() != 0 or cu_seqlens_k[0].item() != 0:
+        raise ValueError("cu_seqlens arrays must start at zero and contain a batch boundary")
+    if (torch.any(cu_seqlens_q[1:] < cu_seqlens_q[:-1]) or
+            torch.any(cu_seqlens_k[1:] < cu_seqlens_k[:-1])):
+        raise ValueError("cu_seqlens arrays must be monotonically non-decreasing")
+    if cu_seqlens_q[-1].item() > q.shape[0] or cu_seqlens_k[-1].item() > k.shape[0]:
+        raise ValueError("cu_seqlens values exceed the packed tensor sizes")
+    if (q.dtype not in (torch.float16, torch.bfloat16, torch.float32) or k.dtype != q.dtype
+            or v.dtype != q.dtype):
+        raise ValueError("flash_attn_varlen_func supports matching FP16, BF16 or FP32 tensors")
+    if not (q.is_cuda and k.is_cuda and v.is_cuda):
+        raise ValueError("All attention tensors must be CUDA tensors")
+    if q.device != k.device or q.device != v.device:
+        raise ValueError("q, k, and v must be on the same CUDA device")
+    if q.shape[-1] != k.shape[-1] or k.shape[-1] != v.shape[-1]:
+        raise ValueError("q, k, and v must have the same head dimension")
+    if q.shape[-1] not in (16, 32, 64, 128, 256):
+        raise ValueError("head dimension must be one of 16, 32, 64, 128, or 256")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError("The number of query heads must be divisible by KV heads")
+    if dropout_p < 0.0 or dropout_p >= 1.0:
+        raise ValueError("dropout_p must be in the range [0, 1)")
+    if softcap < 0.0:
+        raise ValueError("softcap must be non-negative")
+    if cu_seqlens_q.device != q.device or cu_seqlens_k.device != q.device:
+        raise ValueError("cu_seqlens arrays must be on the same CUDA device as q, k, and v")
+    cu_seqlens_q = cu_seqlens_q.to(dtype=torch.int32).contiguous()
+    cu_seqlens_k = cu_seqlens_k.to(dtype=torch.int32).contiguous()
+    if max_seqlen_q < 0 or max_seqlen_k < 0:
+        raise ValueError("max sequence lengths must be non-negative")
+    if cu_seqlens_q[-1].item() != q.shape[0] or cu_seqlens_k[-1].item() != k.shape[0]:
+        raise ValueError("cu_seqlens arrays must cover the packed q and KV tensors")
+    if cu_seqlens_q.numel() < 2:
+        raise ValueError("cu_seqlens arrays must describe at least one sequence")
+    actual_max_q = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item())
+    actual_max_k = int((cu_seqlens_k[1:] - cu_seqlens_k[:-1]).max().item())
+    if max_seqlen_q < actual_max_q or max_seqlen_k < actual_max_k:
+        raise ValueError("max sequence lengths must cover every packed sequence")
+    if max_seqlen_q == 0 or max_seqlen_k == 0:
+        return q.new_zeros((q.shape[0], q.shape[1], q.shape[2]))
+    alibi = _normalize_alibi(alibi_slopes, batch_size, q.shape[1], q.device)
+    use_alibi = alibi is not None and bool(torch.any(alibi != 0))
+    if return_attn_probs:
+        return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
+                                     softcap, alibi)
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    _check_compute_dtype(q.dtype)
+    if softmax_scale is None:
+        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                         softmax_scale=softmax_scale, causal=causal,
+                         window_left=window_size[0], window_right=window_size[1],
+                         softcap=softcap, alibi=alibi if use_alibi else None)
+    return _wrap_grad(out, q, k, v)
+
+
+def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                    max_seqlen_k, dropout_p=0.0, softmax_scale=None,
+                                    causal=False, **kwargs):
+    """Varlen with packed KV (reference :692-699). kv: (total_k, 2, nheads_k, headdim)."""
+    k, v = kv.unbind(dim=1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                  max_seqlen_k, dropout_p=dropout_p,
+                                  softmax_scale=softmax_scale, causal=causal, **kwargs)
+
+
+def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, dropout_p=0.0,
+                                     softmax_scale=None, causal=False, **kwargs):
+    """Varlen with packed QKV (reference :702-708). qkv: (total, 3, nheads, headdim)."""
+    q, k, v = qkv.unbind(dim=1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, max_seqlen, max_seqlen,
+                                  dropout_p=dropout_p, softmax_scale=softmax_scale,
+                                  causal=causal, **kwargs)
+
+
+class FlashSelfAttention(torch.nn.Module):
+    """FlashAttention-compatible self-attention module (reference :711-736)."""
+
+    def __init__(self, causal=False, softmax_scale=None, attention_dropout=0.0,
+                 window_size=(-1, -1), alibi_slopes=None, deterministic=False):
+        super().__init__()
+        self.causal = causal
+        self.softmax_scale = softmax_scale
+        self.drop = torch.nn.Dropout(attention_dropout)
+        self.window_size = window_size
+        self.alibi_slopes = alibi_slopes
+        self.deterministic = deterministic
+
+    def forward(self, qkv, causal=None, cu_seqlens=None, max_seqlen=None):
+        dropout_p = self.drop.p if self.training else 0.0
+        causal = self.causal if causal is None else causal
+        if cu_seqlens is None:
+            return flash_attn_qkvpacked_func(qkv, dropout_p, self.softmax_scale, causal,
+                                             self.window_size, 0.0, self.alibi_slopes,
+                                             self.deterministic)
+        return flash_attn_varlen_qkvpacked_func(
+            qkv, cu_seqlens, max_seqlen, dropout_p, self.softmax_scale, causal,
+            window_size=self.window_size, alibi_slopes=self.alibi_slopes,
+            deterministic=self.deterministic)
+
+
+class FlashCrossAttention(torch.nn.Module):
+    """FlashAttention-compatible cross-attention module (reference :739-770)."""
+
+    def __init__(self, causal=False, softmax_scale=None, attention_dropout=0.0,
+                 window_size=(-1, -1), alibi_slopes=None, deterministic=False):
+        super().__init__()
+        self.causal = causal
+        self.softmax_scale = softmax_scale
+        self.drop = torch.nn.Dropout(attention_dropout)
+        self.window_size = window_size
+        self.alibi_slopes = alibi_slopes
+        self.deterministic = deterministic
+
+    def forward(self, q, kv, causal=None, cu_seqlens=None, max_seqlen=None,
+                cu_seqlens_k=None, max_seqlen_k=None):
+        dropout_p = self.drop.p if self.training else 0.0
+        causal = self.causal if causal is None else causal
+        k, v = kv.unbind(dim=2)
+        if cu_seqlens is None:
+            return flash_attn_func_cross(q, k, v, dropout_p, self.softmax_scale, causal,
+                                         use_native_gqa=not self.training, softcap=0.0,
+                                         alibi_slopes=self.alibi_slopes,
+                                         window_size=self.window_size,
+                                         deterministic=self.deterministic)
+        return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens_k, max_seqlen,
+                                      max_seqlen_k, dropout_p, self.softmax_scale, causal,
+                                      window_size=self.window_size,
+                                      alibi_slopes=self.alibi_slopes,
+                                      deterministic=self.deterministic)
+
+
+class FlashAttention(torch.nn.Module):
+    """Module wrapper of flash_attn_func (reference :773-804)."""
+
+    def __init__(self, attention_dropout=0.0, softmax_scale=None):
+        super().__init__()
+        self.dropout_p = attention_dropout
+        self.softmax_scale = softmax_scale
+
+    def forward(self, q, k, v, causal=False, attn_bias=None):
+        return flash_attn_func(q, k, v, dropout_p=self.dropout_p if self.training else 0.0,
+                               softmax_scale=self.softmax_scale, causal=causal,
+                               attn_bias=attn_bias)
+
+
+__all__ = [
+    "BLOCK_SIZE",
+    "attention",
+    "attention_varlen",
+    "flash_attn_func",
+    "flash_attn_func_cross",
+    "flash_attn_qkvpacked_func",
+    "flash_attn_kvpacked_func",
+    "flash_attn_with_kvcache",
+    "flash_attn_varlen_func",
+    "flash_attn_varlen_kvpacked_func",
+    "flash_attn_varlen_qkvpacked_func",
+    "FlashSelfAttention",
+    "FlashCrossAttention",
+    "FlashAttention",
+]

@@ -1,0 +1,163 @@
+"""Low-level forward launch layer (no Triton inside: the module path is kept for drop-in imports).
+
+Mirrors the public launch functions of the reference's
+``flash_attn_triton/triton_kernel/attention_kernel.py``:
+
+* ``attention``        (reference ``:1201-1259``) - head-major ``[B, H, S, D]`` views.
+* ``attention_varlen`` (reference ``:1364-1380``) - packed ``[T, H, D]`` sequences.
+
+Both call the gfx950 HIP kernels of ``libfa_gfx950.so`` through ``_native``.
+The kernels handle ragged lengths, strided inputs and grouped KV heads
+directly, so nothing is padded, repeated or copied on the host.
+
+Only the forward pass exists.  Calling ``backward`` through these functions
+raises ``NotImplementedError``; dropout is not built either and is rejected
+before launch.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from .. import _native
+
+__all__ = ["attention", "attention_varlen", "dense_forward", "varlen_forward", "FORWARD_ONLY_MSG"]
+
+FORWARD_ONLY_MSG = (
+    "flash_attn_triton (gfx950 HIP build): only the forward pass is implemented; "
+    "the backward kernels are not built yet")
+DROPOUT_MSG = (
+    "flash_attn_triton (gfx950 HIP build): dropout_p > 0 is not implemented; "
+    "call with dropout_p=0.0")
+
+
+class _ForwardOnly(torch.autograd.Function):
+    """Attach a grad_fn that fails loudly: the backward kernels are not built."""
+
+    @staticmethod
+    def forward(ctx, out, *inputs):
+        return out.view_as(out)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        raise NotImplementedError(FORWARD_ONLY_MSG)
+
+
+def _wrap_grad(out: torch.Tensor, *inputs: torch.Tensor) -> torch.Tensor:
+    if torch.is_grad_enabled() and any(t.requires_grad for t in inputs if t is not None):
+        return _ForwardOnly.apply(out, *inputs)
+    return out
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """The kernels read rows with 16-byte loads: unit innermost stride, strides
+    that are multiples of 8 elements and a 16-byte aligned base.  Other layouts
+    get one contiguous copy (the reference copies every non-contiguous input,
+    flash_attn_interface.py:202-204)."""
+    if (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1])
+            and t.data_ptr() % 16 == 0):
+        return t
+    return t.contiguous()
+
+
+def dense_forward(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: int = 0,
+                  window_left: int = -1, window_right: int = -1, softcap: float = 0.0,
+                  alibi: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """Run the dense HIP kernel on ``[B, S, H, D]`` tensors (any BSHD strides).
+
+    Returns ``out [B, Sq, Hq, D]`` (contiguous, dtype of q) and, if requested,
+    the natural-log LSE ``[B, Hq, Sq]`` fp32.
+    """
+    qk, kk, vk = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    B, Sq, Hq, D = q.shape
+    out = torch.empty((B, Sq, Hq, D), dtype=q.dtype, device=q.device)
+    lse = torch.empty((B, Hq, Sq), dtype=torch.float32, device=q.device) if return_lse else None
+    if alibi is not None:
+        alibi = alibi.to(device=q.device, dtype=torch.float32).contiguous()
+    _native.fwd_dense(qk, kk, vk, out, lse, softmax_scale, causal, q_pos_offset, window_left,
+                      window_right, softcap, alibi)
+    return (out, lse) if return_lse else out
+
+
+def varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
+                   softmax_scale: float, causal: bool, window_left: int = -1,
+                   window_right: int = -1, softcap: float = 0.0,
+                   alibi: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """Run the packed varlen HIP kernel on ``[T, H, D]`` tensors."""
+    qk, kk, vk = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
+    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = (torch.empty((q.shape[0], q.shape[1]), dtype=torch.float32, device=q.device)
+           if return_lse else None)
+    if alibi is not None:
+        alibi = alibi.to(device=q.device, dtype=torch.float32).contiguous()
+    cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
+    cu_k = cu_k.to(device=q.device, dtype=torch.int32).contiguous()
+    _native.fwd_varlen(qk, kk, vk, out, lse, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
+                       softmax_scale, causal, window_left, window_right, softcap, alibi)
+    return (out, lse) if return_lse else out
+
+
+def attention(q, k, v, causal=False, sm_scale=None, dropout_p=0.0, dropout_seed=None,
+              seq_len_k=None, seq_len_q=None, kv_heads=None, softcap=0.0, alibi_slopes=None,
+              window_left=-1, window_right=-1, use_alibi=None):
+    """Flash attention forward on head-major views.
+
+    Mirrors ``attention`` (reference attention_kernel.py:1201-1259): q, k, v
+    are ``[batch, heads, seqlen, head_dim]`` with equal, 64-aligned lengths;
+    ``seq_len_k``/``seq_len_q`` give the unpadded lengths (keys at or past
+    ``seq_len_k`` are masked, query row ``i`` sits at position
+    ``i + seq_len_k - seq_len_q``); ``kv_heads`` groups query heads.  Returns
+    ``[batch, heads, seqlen, head_dim]``.
+    """
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    if q.shape[2] != k.shape[2] or k.shape[2] != v.shape[2]:
+        raise ValueError("The low-level attention kernel requires equal sequence lengths")
+    if q.shape[2] % 64 != 0:
+        raise ValueError("The low-level attention kernel requires sequence lengths divisible by 64")
+    if kv_heads is None:
+        kv_heads = k.shape[1]
+    if q.shape[1] % kv_heads != 0:
+        raise ValueError("The number of query heads must be divisible by KV heads")
+    head_dim_q, head_dim_k, head_dim_v = q.shape[-1], k.shape[-1], v.shape[-1]
+    assert head_dim_q == head_dim_k == head_dim_v
+    assert head_dim_k in {16, 32, 64, 128, 256}
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    if alibi_slopes is None:
+        use_alibi = False
+    elif use_alibi is None:
+        use_alibi = bool(torch.any(alibi_slopes != 0))
+    if seq_len_k is None:
+        seq_len_k = q.shape[2]
+    if seq_len_q is None:
+        seq_len_q = q.shape[2]
+    alibi = None
+    if use_alibi:
+        alibi = alibi_slopes.reshape(-1, q.shape[1]).expand(q.shape[0], -1)
+    out = dense_forward(
+        q.transpose(1, 2), k.transpose(1, 2)[:, :seq_len_k], v.transpose(1, 2)[:, :seq_len_k],
+        softmax_scale=sm_scale, causal=causal, q_pos_offset=seq_len_k - seq_len_q,
+        window_left=window_left, window_right=window_right, softcap=softcap, alibi=alibi)
+    return _wrap_grad(out.transpose(1, 2), q, k, v)
+
+
+def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                     causal=False, sm_scale=None, dropout_p=0.0, dropout_seed=None, softcap=0.0,
+                     alibi_slopes=None, window_left=-1, window_right=-1, use_alibi=None):
+    """Packed variable-length forward (reference attention_kernel.py:1364-1380)."""
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    if alibi_slopes is None:
+        use_alibi = False
+    elif use_alibi is None:
+        use_alibi = bool(torch.any(alibi_slopes != 0))
+    out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                         softmax_scale=sm_scale, causal=causal, window_left=window_left,
+                         window_right=window_right, softcap=softcap,
+                         alibi=alibi_slopes if use_alibi else None)
+    return _wrap_grad(out, q, k, v)

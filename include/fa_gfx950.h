@@ -1,0 +1,157 @@
+/* C ABI of libfa_gfx950.so: FlashAttention-2 forward kernels for AMD MI355X (gfx950).
+ *
+ * Every entry point takes raw device pointers, element strides, sizes and the
+ * HIP stream to launch on, and returns an int status (FA_OK on success).  No
+ * entry point allocates device memory: outputs and workspaces are provided by
+ * the caller.  Launches are asynchronous on `stream`.  On failure
+ * fa_last_error_string() describes the error for the calling thread.
+ *
+ * The reference (luyanaa/flash-attn-triton) is pure Python + Triton; it has no
+ * FFI.  Each function below replaces one Triton launch site of the reference's
+ * forward path (cited per function); the Python layer of this package
+ * (flash_attn_triton/) calls these through ctypes at exactly those sites.
+ *
+ * Tensor layouts.  `dtype` is FA_DTYPE_F16 or FA_DTYPE_BF16.  Strides are in
+ * elements and the innermost (head-dim) stride must be 1.
+ */
+#ifndef FA_GFX950_H_
+#define FA_GFX950_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* fa_stream_t; /* == hipStream_t */
+
+#define FA_OK 0
+#define FA_ERR_INVALID 1     /* argument rejected before any launch */
+#define FA_ERR_UNSUPPORTED 2 /* shape/dtype combination not built */
+#define FA_ERR_HIP 3         /* HIP runtime reported an error */
+
+#define FA_DTYPE_F16 0
+#define FA_DTYPE_BF16 1
+
+/* Library version (major*10000 + minor*100 + patch). */
+int fa_version(void);
+
+/* Description of the last error raised on the calling thread ("" if none). */
+const char* fa_last_error_string(void);
+
+/* Dense (and cross) forward attention on [B, S, H, D] strided tensors.
+ *
+ * Replaces the `_attn_fwd[grid](...)` launch of
+ * flash_attn_triton/triton_kernel/attention_kernel.py:1082 (through
+ * `_launch_dense_forward`, :1057-1101, and `attention`, :1201-1259).
+ *
+ * q [B, Sq, Hq, D], k/v [B, Sk, Hk, D], out [B, Sq, Hq, D]; *_stride[3] =
+ * {batch, seq, head} element strides.  Hq % Hk == 0; query head h reads KV
+ * head h / (Hq / Hk).  Query row i sits at position i + q_pos_offset; keys are
+ * at positions 0..Sk-1 (upper-left alignment when the offset is 0).
+ * causal keeps kpos <= qpos; window_left/right >= 0 keep
+ * qpos-left <= kpos <= qpos+right (negative = unbounded).  alibi_slopes
+ * (nullable, fp32) holds slope[b * alibi_batch_stride + h]; softcap > 0 caps
+ * scores with softcap*tanh(s/softcap).  lse (nullable, fp32) receives the
+ * natural-log logsumexp at lse[b*lse_stride[0] + h*lse_stride[1] +
+ * i*lse_stride[2]]; rows with no visible key get out = 0 and lse = -inf.
+ */
+int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* lse,
+                 int64_t batch, int64_t seqlen_q, int64_t seqlen_k, int64_t heads_q,
+                 int64_t heads_k, int64_t head_dim, const int64_t* q_stride,
+                 const int64_t* k_stride, const int64_t* v_stride, const int64_t* o_stride,
+                 const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                 int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
+                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream);
+
+/* Packed variable-length forward attention.
+ *
+ * Replaces the `_varlen_fwd[grid](...)` launch of attention_kernel.py:1298
+ * (through `_attention_varlen.forward`, :1283-1320).  q [Tq, Hq, D],
+ * k/v [Tk, Hk, D] with *_stride[2] = {token, head}; sequence b owns query
+ * rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) and key rows
+ * [cu_seqlens_k[b], cu_seqlens_k[b+1]) (device int32 arrays of batch+1
+ * entries); positions are local to each sequence.  max_seqlen_q must bound
+ * every query length.  lse (nullable) is [Tq, Hq] at
+ * lse[t*lse_stride[0] + h*lse_stride[1]].  Other arguments as fa_fwd_dense.
+ */
+int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float* lse,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t heads_q, int64_t heads_k,
+                  int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride, const int64_t* lse_stride,
+                  int dtype, float softmax_scale, int causal, int64_t window_left,
+                  int64_t window_right, float softcap, const float* alibi_slopes,
+                  int64_t alibi_batch_stride, fa_stream_t stream);
+
+/* Split-KV plan for fa_fwd_kvcache: the number of key splits the launch will
+ * use and the workspace bytes it needs (0 when num_splits == 1).
+ * max_keys bounds every sequence's visible key count (e.g. the cache
+ * capacity).  Host-only, no device work.
+ */
+int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
+                        int64_t head_dim, int64_t max_keys, int32_t* num_splits,
+                        int64_t* workspace_bytes);
+
+/* Attention of q against a KV cache, paged or batched (decode and chunked
+ * prefill against a cache).
+ *
+ * Replaces the per-sequence Python loop of
+ * flash_attn_triton/flash_attn_interface.py:501-525 (gather + pad +
+ * `flash_attn_func_cross` + `_attn_fwd` launch per batch item) with one
+ * split-KV launch plus a combine launch.
+ *
+ * q [B, Sq, Hq, D] (q_stride {batch, seq, head}); out likewise.
+ * Paged (block_table != NULL): k_cache/v_cache [num_pages, page_size, Hk, D]
+ * with cache_stride {page, slot, head}; logical key t of sequence b lives in
+ * page block_table[b*block_table_stride + t/page_size], slot t%page_size.
+ * Batched (block_table == NULL): caches [rows, capacity, Hk, D] with
+ * cache_stride {row, slot, head}; sequence b reads cache row
+ * cache_batch_idx[b] (nullable: b) from slot cache_leftpad[b] (nullable: 0).
+ * cache_seqlens[b] (device int32, nullable: max_keys for every b) visible
+ * keys.  When causal, query i sits at position i + L_b - Sq (bottom-right);
+ * otherwise at i.  window/alibi as fa_fwd_dense.  lse (nullable) is
+ * [B, Hq, Sq] at lse[b*s0 + h*s1 + i*s2].  num_splits/workspace come from
+ * fa_fwd_kvcache_plan (workspace may be NULL when its size is 0).
+ */
+int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void* out,
+                   float* lse, const int32_t* cache_seqlens, const int32_t* block_table,
+                   int64_t block_table_stride, int64_t page_size, const int32_t* cache_batch_idx,
+                   const int32_t* cache_leftpad, int64_t batch, int64_t seqlen_q,
+                   int64_t max_keys, int64_t heads_q, int64_t heads_k, int64_t head_dim,
+                   const int64_t* q_stride, const int64_t* k_cache_stride,
+                   const int64_t* v_cache_stride, const int64_t* o_stride,
+                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                   int64_t window_left, int64_t window_right, const float* alibi_slopes,
+                   int64_t alibi_batch_stride, int32_t num_splits, void* workspace,
+                   int64_t workspace_bytes, fa_stream_t stream);
+
+/* Per-token INT8 quantization of K (fp16), bit-exact with
+ * `_quantize_k_rows` (attention_kernel_int8.py:58-79, launched at :232):
+ *   s = fp32(max(amax_row, 1)) / 127;  k8 = round_half_away(fp32(k) * (1/s)).
+ * k [B, H, S, D] fp16 with k_stride {batch, head, seq}; k8 [B*H, S, D] int8
+ * contiguous; s_k [B*H, S] fp32.  D in {32, 64, 128, 256}.
+ */
+int fa_quant_k_int8(const void* k, int8_t* k8, float* s_k, int64_t batch, int64_t heads,
+                    int64_t seqlen, int64_t head_dim, const int64_t* k_stride,
+                    fa_stream_t stream);
+
+/* INT8-QK^T attention forward (`_attn_fwd_int8`, attention_kernel_int8.py:167-217,
+ * launched at :237).  q/v/out [B, H, S, D] fp16 with strides
+ * {batch, head, seq}; k8/s_k from fa_quant_k_int8.  Q is quantized per row in
+ * the kernel (division form); QK^T runs on int8 MFMA with i32 accumulation,
+ * PV on fp16 MFMA.  Keys >= seq_len_k are masked; for causal, query i sits at
+ * position i + seq_len_k - seq_len_q.  lse (nullable) receives the natural-log
+ * logsumexp [B, H, S] contiguous.
+ */
+int fa_fwd_int8(const void* q, const int8_t* k8, const float* s_k, const void* v, void* out,
+                float* lse, int64_t batch, int64_t heads, int64_t seqlen, int64_t head_dim,
+                const int64_t* q_stride, const int64_t* v_stride, const int64_t* o_stride,
+                float sm_scale, int causal, int64_t seq_len_k, int64_t seq_len_q,
+                fa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FA_GFX950_H_ */

@@ -1,0 +1,166 @@
+"""Parity of the dense / cross HIP forward against the float64 oracle.
+
+Covers what the reference's tests exercise (equal length, causal, window,
+rectangular cross, ALiBi, non-contiguous packed slices; reference
+tests/test_compare_implementations.py:85-212) plus what they leave out:
+every supported head dim, bf16, GQA, softcap, ragged lengths, empty rows
+and the LSE.  Full-size BASELINE shapes are checked on sampled rows.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import ATOL, assert_close, randn, to_np
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _run(q, k, v, **kw):
+    from flash_attn_triton.triton_kernel.attention_kernel import dense_forward
+    scale = kw.pop("softmax_scale", 1.0 / math.sqrt(q.shape[-1]))
+    out, lse = dense_forward(q.to(DEV), k.to(DEV), v.to(DEV), softmax_scale=scale,
+                             return_lse=True, **kw)
+    torch.cuda.synchronize()
+    return out.cpu(), lse.cpu()
+
+
+def _oracle(q, k, v, softmax_scale=None, causal=False, q_pos_offset=0, window_left=-1,
+            window_right=-1, softcap=0.0, alibi=None):
+    out, lse, _ = ora.attention(to_np(q), to_np(k), to_np(v), softmax_scale, causal,
+                                (window_left, window_right), softcap,
+                                None if alibi is None else to_np(alibi),
+                                causal_offset=q_pos_offset)
+    return out, lse
+
+
+def _check(q, k, v, dtype=torch.float16, **kw):
+    out, lse = _run(q, k, v, **dict(kw))
+    ref_out, ref_lse = _oracle(q, k, v, **kw)
+    assert_close(to_np(out), ref_out, ATOL[dtype], "out", dtype)
+    assert_close(lse.numpy(), ref_lse, 1e-3, "lse")
+
+
+@pytest.mark.parametrize("head_dim", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_head_dims(head_dim, causal, dtype):
+    B, S, H = 2, 200, 3
+    q = randn((B, S, H, head_dim), 1, dtype)
+    k = randn((B, S, H, head_dim), 2, dtype)
+    v = randn((B, S, H, head_dim), 3, dtype)
+    _check(q, k, v, dtype, causal=causal)
+
+
+@pytest.mark.parametrize("sq,sk", [(1, 1), (7, 13), (13, 7), (17, 17), (130, 64), (64, 333),
+                                   (333, 64), (257, 1000)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_ragged_and_rectangular(sq, sk, causal):
+    q = randn((2, sq, 2, 64), 11)
+    k = randn((2, sk, 2, 64), 12)
+    v = randn((2, sk, 2, 64), 13)
+    _check(q, k, v, causal=causal)
+
+
+@pytest.mark.parametrize("hq,hk", [(8, 2), (8, 1), (6, 3)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa(hq, hk, causal):
+    q = randn((2, 150, hq, 128), 21)
+    k = randn((2, 150, hk, 128), 22)
+    v = randn((2, 150, hk, 128), 23)
+    _check(q, k, v, causal=causal)
+
+
+@pytest.mark.parametrize("window", [(3, 2), (64, 0), (-1, 16), (100, -1), (0, 0), (200, 300)])
+@pytest.mark.parametrize("causal", [False, True])
+def test_window(window, causal):
+    q = randn((1, 300, 2, 64), 31)
+    k = randn((1, 300, 2, 64), 32)
+    v = randn((1, 300, 2, 64), 33)
+    _check(q, k, v, causal=causal, window_left=window[0], window_right=window[1])
+
+
+@pytest.mark.parametrize("per_batch", [False, True])
+def test_alibi(per_batch):
+    B, S, H = 2, 190, 4
+    q, k, v = (randn((B, S, H, 64), s) for s in (41, 42, 43))
+    gen = torch.Generator().manual_seed(44)
+    if per_batch:
+        slopes = torch.rand(B, H, generator=gen) * 0.5
+    else:
+        slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).expand(B, H).contiguous()
+    _check(q, k, v, causal=True, alibi=slopes.float())
+    _check(q, k, v, causal=False, alibi=slopes.float())
+
+
+@pytest.mark.parametrize("softcap", [30.0, 1.0, 0.05])
+def test_softcap(softcap):
+    q, k, v = (randn((2, 160, 2, 128), s, scale=2.0) for s in (51, 52, 53))
+    _check(q, k, v, causal=True, softcap=softcap)
+
+
+def test_all_features_together():
+    H = 4
+    q, k, v = (randn((2, 500, H, 128), s) for s in (61, 62, 63))
+    slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).expand(2, H).contiguous().float()
+    _check(q, k, v, causal=True, window_left=100, window_right=0, softcap=30.0, alibi=slopes)
+
+
+def test_empty_rows_give_zero_and_neg_inf_lse():
+    # Query rows at negative positions see no key under a causal mask.
+    q, k, v = (randn((1, 40, 2, 64), s) for s in (71, 72, 73))
+    out, lse = _run(q, k, v, causal=True, q_pos_offset=-10)
+    assert torch.all(out[:, :10] == 0)
+    assert torch.all(torch.isneginf(lse[:, :, :10]))
+    ref_out, ref_lse = _oracle(q, k, v, causal=True, q_pos_offset=-10)
+    assert_close(to_np(out), ref_out, ATOL[torch.float16], "out", torch.float16)
+    assert_close(lse.numpy(), ref_lse, 1e-3, "lse")
+
+
+def test_uniform_attention_is_mean_of_v():
+    # q = 0 makes every visible key equally likely: out = mean of the visible V rows.
+    k = randn((1, 96, 2, 64), 81)
+    v = randn((1, 96, 2, 64), 82)
+    q = torch.zeros((1, 96, 2, 64), dtype=torch.float16)
+    out, lse = _run(q, k, v, causal=False)
+    vm = to_np(v).mean(axis=1, keepdims=True)
+    assert_close(to_np(out), np.broadcast_to(vm, out.shape), 1e-3, "mean")
+    assert_close(lse.numpy(), np.full(lse.shape, math.log(96)), 1e-4, "lse")
+
+
+def test_strided_packed_slices():
+    # The geometry flash_attn_qkvpacked_func hands over (reference test :181-191).
+    q, k, v = (randn((2, 128, 2, 64), s) for s in (91, 92, 93))
+    packed = torch.stack((q, k, v), dim=2).to(DEV)
+    qs, ks, vs = packed.unbind(dim=2)
+    assert not qs.is_contiguous()
+    from flash_attn_triton.triton_kernel.attention_kernel import dense_forward
+    out = dense_forward(qs, ks, vs, softmax_scale=0.125, causal=True).cpu()
+    ref, _ = _oracle(q, k, v, softmax_scale=0.125, causal=True)
+    assert_close(to_np(out), ref, ATOL[torch.float16], "packed", torch.float16)
+
+
+def _sampled_rows_check(q, k, v, causal, n_rows=48, seed=5):
+    """Full-size check on a sample of (batch, head, row) triples."""
+    out = _run(q, k, v, causal=causal)[0]
+    B, S, H, D = q.shape
+    rng = np.random.default_rng(seed)
+    for _ in range(n_rows):
+        b, h = int(rng.integers(B)), int(rng.integers(H))
+        i = int(rng.choice([0, S - 1, int(rng.integers(S))]))
+        ref, _, _ = ora.attention(to_np(q[b:b + 1, i:i + 1, h:h + 1]), to_np(k[b:b + 1, :, h:h + 1]),
+                                  to_np(v[b:b + 1, :, h:h + 1]), causal=causal, causal_offset=i)
+        assert_close(to_np(out[b:b + 1, i:i + 1, h:h + 1]), ref, ATOL[torch.float16],
+                     f"row b={b} h={h} i={i}", torch.float16)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_baseline_config_c2_sampled(causal):
+    # B=4, H=32, S=4096, D=128 fp16.
+    B, S, H, D = 4, 4096, 32, 128
+    q, k, v = (randn((B, S, H, D), s) for s in (1, 2, 3))
+    _sampled_rows_check(q, k, v, causal)

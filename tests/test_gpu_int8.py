@@ -1,0 +1,115 @@
+"""INT8-QK path on the GPU: byte-exact K quantization and attention parity."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import INT8_ATOL, assert_close, randn, to_np
+from oracle import attention as ora
+from oracle import quant
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _outlier_k(B, H, S, D, seed):
+    """K ~ N(0,1) fp16 with 1% of token rows scaled x8."""
+    k = randn((B, H, S, D), seed)
+    gen = torch.Generator().manual_seed(seed + 1000)
+    n_out = max(1, S // 100)
+    for b in range(B):
+        for h in range(H):
+            rows = torch.randperm(S, generator=gen)[:n_out]
+            k[b, h, rows] = (k[b, h, rows].float() * 8.0).half()
+    return k
+
+
+@pytest.mark.parametrize("head_dim", [32, 64, 128, 256])
+def test_quant_k_byte_exact(head_dim):
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import quantize_k_int8
+    k = _outlier_k(2, 3, 320, head_dim, 5)
+    # add rows that hit the clamp, exact zeros and x.5 ties
+    k[0, 0, 0] = 0
+    k[0, 0, 1] = torch.linspace(-0.9, 0.9, head_dim).half()
+    k8, s_k = quantize_k_int8(k.to(DEV))
+    torch.cuda.synchronize()
+    ref8, refs = quant.quantize_k_rows(k.numpy().reshape(-1, 320, head_dim))
+    assert np.array_equal(k8.cpu().numpy(), ref8)
+    assert np.array_equal(s_k.cpu().numpy().view(np.uint32), refs.view(np.uint32))
+
+
+def test_quant_k_strided_input():
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import quantize_k_int8
+    base = _outlier_k(2, 128, 4, 64, 9)            # [B, S, H, D] storage
+    k = base.transpose(1, 2)                        # [B, H, S, D] view
+    k8, s_k = quantize_k_int8(k.to(DEV))
+    ref8, refs = quant.quantize_k_rows(k.contiguous().numpy().reshape(-1, 128, 64))
+    assert np.array_equal(k8.cpu().numpy(), ref8)
+    assert np.array_equal(s_k.cpu().numpy(), refs)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_int8_attention(causal, head_dim):
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import attention_int8
+    B, H, S = 2, 2, 384
+    q = randn((B, H, S, head_dim), 1)
+    k = _outlier_k(B, H, S, head_dim, 2)
+    v = randn((B, H, S, head_dim), 3)
+    out = attention_int8(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal).cpu()
+    # Parity bar: the INT8-QK semantics (per-token quantized Q and K, exact
+    # integer QK^T, float64 softmax and PV) at 2e-2.
+    ref, _ = quant.attention_int8(q.numpy(), k.numpy(), to_np(v), causal=causal)
+    assert_close(to_np(out), ref, INT8_ATOL, "int8 vs INT8-semantics oracle", torch.float16)
+    # The scheme itself moves the result away from unquantized attention: with
+    # x8 outlier keys the oracle-vs-oracle distance reaches ~0.2 on some rows.
+    # The kernel must not add to it beyond the fp16 bar.
+    ref_f, _, _ = ora.attention(to_np(q.transpose(1, 2)), to_np(k.transpose(1, 2)),
+                                to_np(v.transpose(1, 2)), causal=causal)
+    scheme = np.abs(ref - ref_f.transpose(0, 2, 1, 3))
+    kernel = np.abs(to_np(out) - ref_f.transpose(0, 2, 1, 3))
+    assert np.max(kernel - scheme) <= 2e-3 + 1e-3
+
+
+def test_int8_reference_case():
+    # Reference tests/test_compare_implementations.py:222-235 (forward part):
+    # B=2, S=128, H=2, D=64, scale 0.125, causal and not.
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import attention_int8
+    q, k, v = (randn((2, 128, 2, 64), s) for s in (42, 43, 44))
+    for causal in (False, True):
+        out = attention_int8(*(t.transpose(1, 2).contiguous().to(DEV) for t in (q, k, v)),
+                             causal=causal, sm_scale=0.125).transpose(1, 2).cpu()
+        ref, _, _ = ora.attention(to_np(q), to_np(k), to_np(v), 0.125, causal)
+        assert_close(to_np(out), ref, INT8_ATOL, f"causal={causal}")
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_int8_baseline_c3_sampled(causal):
+    # B=4, H=32, S=4096, D=128, 1% outlier K rows; sampled rows.
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import (attention_int8,
+                                                                      quantize_k_int8)
+    B, H, S, D = 4, 32, 4096, 128
+    q = randn((B, H, S, D), 4)
+    k = randn((B, H, S, D), 5)
+    gen = torch.Generator().manual_seed(6)
+    for b in range(B):
+        for h in range(H):
+            rows = torch.randperm(S, generator=gen)[:41]
+            k[b, h, rows] = (k[b, h, rows].float() * 8.0).half()
+    v = randn((B, H, S, D), 7)
+    kd = k.to(DEV)
+    k8, s_k = quantize_k_int8(kd)
+    ref8, refs = quant.quantize_k_rows(k.numpy().reshape(B * H, S, D))
+    assert np.array_equal(k8.cpu().numpy(), ref8)
+    assert np.array_equal(s_k.cpu().numpy(), refs)
+    out = attention_int8(q.to(DEV), kd, v.to(DEV), causal=causal).cpu()
+    rng = np.random.default_rng(3)
+    for _ in range(24):
+        b, h, i = int(rng.integers(B)), int(rng.integers(H)), int(rng.integers(S))
+        ref, _ = quant.attention_int8(q[b:b + 1, h:h + 1, i:i + 1].numpy(),
+                                      k[b:b + 1, h:h + 1].numpy(), to_np(v[b:b + 1, h:h + 1]),
+                                      causal=causal, q_positions=[i])
+        assert_close(to_np(out[b, h, i]), ref[0, 0, 0], INT8_ATOL, f"b={b} h={h} i={i}",
+                     torch.float16)

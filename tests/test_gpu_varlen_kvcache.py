@@ -1,0 +1,157 @@
+"""Parity of the varlen and KV-cache HIP paths against the float64 oracle."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import ATOL, assert_close, randn, to_np
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def _cu(lengths):
+    return torch.tensor(np.concatenate([[0], np.cumsum(lengths)]), dtype=torch.int32)
+
+
+def _varlen_case(lq, lk, hq=4, hk=4, d=64, seed=0, dtype=torch.float16, **kw):
+    from flash_attn_triton.triton_kernel.attention_kernel import varlen_forward
+    cu_q, cu_k = _cu(lq), _cu(lk)
+    q = randn((int(sum(lq)), hq, d), seed + 1, dtype)
+    k = randn((int(sum(lk)), hk, d), seed + 2, dtype)
+    v = randn((int(sum(lk)), hk, d), seed + 3, dtype)
+    scale = kw.pop("softmax_scale", 1.0 / math.sqrt(d))
+    alibi = kw.pop("alibi", None)
+    out, lse = varlen_forward(q.to(DEV), k.to(DEV), v.to(DEV), cu_q.to(DEV), cu_k.to(DEV),
+                              max(lq), max(lk), softmax_scale=scale, return_lse=True,
+                              alibi=None if alibi is None else alibi.to(DEV), **kw)
+    torch.cuda.synchronize()
+    ref_out, ref_lse = ora.attention_varlen(
+        to_np(q), to_np(k), to_np(v), cu_q.numpy(), cu_k.numpy(), scale, kw.get("causal", False),
+        (kw.get("window_left", -1), kw.get("window_right", -1)), kw.get("softcap", 0.0),
+        None if alibi is None else to_np(alibi))
+    assert_close(to_np(out.cpu()), ref_out, ATOL[dtype], "varlen out", dtype)
+    assert_close(lse.cpu().numpy(), ref_lse, 1e-3, "varlen lse")
+
+
+def test_reference_varlen_case():
+    # Reference tests/test_compare_implementations.py:140-159: cu_q=[0,3,8], cu_k=[0,4,10].
+    _varlen_case([3, 5], [4, 6], hq=2, hk=2, d=16, causal=True)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_ragged(causal):
+    _varlen_case([1, 130, 64, 257, 5], [3, 130, 200, 100, 5], causal=causal, seed=10)
+
+
+def test_varlen_empty_sequences():
+    # Zero-length query and key sequences inside the batch.
+    _varlen_case([0, 20, 33, 7], [5, 0, 40, 7], causal=False, seed=20)
+    _varlen_case([0, 20, 33, 7], [5, 0, 40, 7], causal=True, seed=21)
+
+
+def test_varlen_gqa_window_alibi_softcap():
+    H = 8
+    slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).expand(3, H).contiguous().float()
+    _varlen_case([300, 129, 513], [300, 129, 513], hq=H, hk=2, d=128, causal=True,
+                 window_left=64, window_right=0, softcap=30.0, alibi=slopes, seed=30)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_varlen_baseline_c5_features(dtype):
+    # BASELINE config 5 (reduced to 6 sequences so the float64 oracle stays quick):
+    # causal, window (1024, 0), ALiBi 2^(-8(i+1)/H), softcap 30, H=16, D=128.
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(128, 4097, (6,), generator=gen).tolist()
+    H = 16
+    slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).expand(6, H).contiguous().float()
+    _varlen_case(lengths, lengths, hq=H, hk=H, d=128, causal=True, window_left=1024,
+                 window_right=0, softcap=30.0, alibi=slopes, seed=40, dtype=dtype)
+
+
+def _paged_setup(lengths, page_size, hk, d, seed, dtype=torch.float16, extra_pages=3):
+    pages_per = [(L + page_size - 1) // page_size for L in lengths]
+    n_pages = sum(pages_per) + extra_pages
+    gen = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(n_pages, generator=gen)
+    max_pages = max(pages_per) if pages_per else 1
+    bt = torch.zeros((len(lengths), max_pages), dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(pages_per):
+        bt[b, :n] = perm[pos:pos + n].to(torch.int32)
+        pos += n
+    kc = randn((n_pages, page_size, hk, d), seed + 1, dtype)
+    vc = randn((n_pages, page_size, hk, d), seed + 2, dtype)
+    return kc, vc, bt
+
+
+@pytest.mark.parametrize("sq", [1, 2, 9])
+@pytest.mark.parametrize("causal", [False, True])
+def test_paged_kvcache(sq, causal):
+    from flash_attn_triton import flash_attn_with_kvcache
+    lengths = [1, 37, 256, 700, 1500, 2049]
+    page, hq, hk, d = 256, 8, 2, 128
+    kc, vc, bt = _paged_setup(lengths, page, hk, d, seed=100)
+    q = randn((len(lengths), sq, hq, d), 103)
+    seqlens = torch.tensor(lengths, dtype=torch.int32)
+    out = flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_seqlens=seqlens.to(DEV),
+                                  block_table=bt.to(DEV), causal=causal)
+    torch.cuda.synchronize()
+    ref, _, _, _ = ora.attention_kvcache(to_np(q), to_np(kc), to_np(vc), cache_seqlens=lengths,
+                                         block_table=bt.numpy(), causal=causal)
+    assert_close(to_np(out.cpu()), ref, ATOL[torch.float16], "paged", torch.float16)
+
+
+def test_batched_cache_with_rows_and_leftpad():
+    from flash_attn_triton import flash_attn_with_kvcache
+    B, cap, hq, hk, d = 3, 300, 4, 4, 64
+    kc = randn((5, cap, hk, d), 111)
+    vc = randn((5, cap, hk, d), 112)
+    q = randn((B, 3, hq, d), 113)
+    rows = torch.tensor([4, 0, 2], dtype=torch.int32)
+    leftpad = torch.tensor([0, 17, 100], dtype=torch.int32)
+    lengths = torch.tensor([300, 200, 1], dtype=torch.int32)
+    for causal in (False, True):
+        out = flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV),
+                                      cache_seqlens=lengths.to(DEV), cache_batch_idx=rows.to(DEV),
+                                      cache_leftpad=leftpad.to(DEV), causal=causal,
+                                      window_size=(50, -1))
+        torch.cuda.synchronize()
+        ref, _, _, _ = ora.attention_kvcache(to_np(q), to_np(kc), to_np(vc),
+                                             cache_seqlens=lengths.numpy(),
+                                             cache_batch_idx=rows.numpy(),
+                                             cache_leftpad=leftpad.numpy(), causal=causal,
+                                             window_size=(50, -1))
+        assert_close(to_np(out.cpu()), ref, ATOL[torch.float16], f"batched causal={causal}",
+                     torch.float16)
+
+
+def test_paged_decode_baseline_c4_sampled():
+    # 64 sequences, L ~ U[512, 8192], page 256, Hq 32, Hk 8, D 128.
+    from flash_attn_triton import flash_attn_with_kvcache
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(512, 8193, (64,), generator=gen)
+    page, hq, hk, d = 256, 32, 8, 128
+    pages_per = ((lengths + page - 1) // page).tolist()
+    n_pages = sum(pages_per)
+    perm = torch.randperm(n_pages, generator=gen)
+    bt = torch.zeros((64, 32), dtype=torch.int32)
+    pos = 0
+    for b, n in enumerate(pages_per):
+        bt[b, :n] = perm[pos:pos + n].to(torch.int32)
+        pos += n
+    kc = randn((n_pages, page, hk, d), 7)
+    vc = randn((n_pages, page, hk, d), 8)
+    q = randn((64, 1, hq, d), 9)
+    out = flash_attn_with_kvcache(q.to(DEV), kc.to(DEV), vc.to(DEV),
+                                  cache_seqlens=lengths.to(torch.int32).to(DEV),
+                                  block_table=bt.to(DEV), causal=False).cpu()
+    for b in (0, 17, 63):
+        ref, _, _, _ = ora.attention_kvcache(to_np(q[b:b + 1]), to_np(kc), to_np(vc),
+                                             cache_seqlens=[int(lengths[b])],
+                                             block_table=bt[b:b + 1].numpy(), causal=False)
+        assert_close(to_np(out[b:b + 1]), ref, ATOL[torch.float16], f"decode b={b}",
+                     torch.float16)

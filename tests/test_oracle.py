@@ -1,0 +1,414 @@
+"""Pins the CPU oracle before anything is compared against it (CPU only).
+
+Each oracle function is checked against something independent of its own
+formula: torch's CPU ``scaled_dot_product_attention`` (the oracle of the
+reference's tests, tests/test_compare_implementations.py:31-41, with window
+and ALiBi expressed as SDPA masks/biases as at :97-105 and :208-211), closed
+forms, a pure-Python brute force on tiny shapes, exact rational arithmetic
+for the quantizer, and a second (C) implementation of the quantizer.
+"""
+import ctypes
+import math
+import os
+import subprocess
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import attention as ora
+from oracle import quant
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _sdpa(q, k, v, causal=False, scale=None, mask=None, gqa=False):
+    """SDPA in float64 on [B,S,H,D] numpy inputs -> [B,S,H,D]."""
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).double().transpose(1, 2)
+    out = F.scaled_dot_product_attention(t(q), t(k), t(v), attn_mask=mask, is_causal=causal,
+                                         scale=scale, enable_gqa=gqa)
+    return out.transpose(1, 2).numpy()
+
+
+def _rand(shape, seed):
+    return np.random.default_rng(seed).standard_normal(shape)
+
+
+# ----------------------------------------------------------------- attention vs SDPA
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq,sk", [(17, 17), (7, 13), (13, 7), (64, 64)])
+def test_attention_matches_sdpa(causal, sq, sk):
+    q, k, v = _rand((2, sq, 3, 16), 1), _rand((2, sk, 3, 16), 2), _rand((2, sk, 3, 16), 3)
+    out, lse, probs = ora.attention(q, k, v, 0.125, causal)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, causal, 0.125), atol=1e-12)
+    # LSE is consistent with the probabilities: p = exp(s - lse) sums to one.
+    np.testing.assert_allclose(probs.sum(-1), 1.0, atol=1e-12)
+
+
+def test_attention_gqa_matches_sdpa():
+    q, k, v = _rand((2, 20, 8, 32), 4), _rand((2, 20, 2, 32), 5), _rand((2, 20, 2, 32), 6)
+    out, _, _ = ora.attention(q, k, v, None, True)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, True, 1 / math.sqrt(32), gqa=True), atol=1e-12)
+
+
+def test_default_scale_is_inverse_sqrt_d():
+    q, k, v = _rand((1, 9, 2, 64), 7), _rand((1, 9, 2, 64), 8), _rand((1, 9, 2, 64), 9)
+    out, _, _ = ora.attention(q, k, v)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, False, 0.125), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("window", [(3, 2), (0, 0), (5, -1), (-1, 1)])
+def test_window_matches_sdpa_mask(causal, window):
+    # Reference tests/test_compare_implementations.py:93-130 builds the same mask.
+    q, k, v = _rand((1, 17, 2, 16), 10), _rand((1, 17, 2, 16), 11), _rand((1, 17, 2, 16), 12)
+    pos = torch.arange(17)
+    valid = torch.ones(17, 17, dtype=torch.bool)
+    if window[0] >= 0:
+        valid &= pos[None, :] >= pos[:, None] - window[0]
+    if window[1] >= 0:
+        valid &= pos[None, :] <= pos[:, None] + window[1]
+    if causal:
+        valid &= pos[None, :] <= pos[:, None]
+    out, _, _ = ora.attention(q, k, v, None, causal, window)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, mask=valid), atol=1e-12)
+
+
+def test_alibi_matches_sdpa_bias():
+    # Reference tests/test_compare_implementations.py:204-212.
+    q, k, v = _rand((2, 17, 2, 16), 13), _rand((2, 17, 2, 16), 14), _rand((2, 17, 2, 16), 15)
+    slopes = np.abs(_rand((2, 2), 16)) * 0.1
+    qp, kp = torch.arange(17)[:, None], torch.arange(17)[None, :]
+    bias = -torch.from_numpy(slopes)[:, :, None, None] * (qp - kp).abs().double()
+    out, _, _ = ora.attention(q, k, v, None, False, alibi_slopes=slopes)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, mask=bias), atol=1e-12)
+    # (H,) slopes broadcast over the batch
+    out1, _, _ = ora.attention(q, k, v, None, True, alibi_slopes=slopes[0])
+    bias1 = bias[:1].expand(2, -1, -1, -1) + torch.where(qp >= kp, 0.0, -math.inf)
+    np.testing.assert_allclose(out1, _sdpa(q, k, v, mask=bias1), atol=1e-12)
+
+
+def test_attn_bias_matches_sdpa():
+    # Reference tests/test_compare_implementations.py:171-178.
+    q, k, v = _rand((2, 7, 2, 16), 17), _rand((2, 13, 2, 16), 18), _rand((2, 13, 2, 16), 19)
+    bias = _rand((2, 2, 7, 13), 20) * 0.1
+    out, _, _ = ora.attention(q, k, v, attn_bias=bias)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, mask=torch.from_numpy(bias)), atol=1e-12)
+
+
+# ----------------------------------------------------------------- closed forms
+def test_softcap_saturates_to_known_probabilities():
+    # scores +-100 with cap 1: capped scores are tanh(+-100) = +-1 (to 1e-80), so
+    # the two probabilities are e/(e + 1/e) and (1/e)/(e + 1/e).
+    D = 4
+    q = np.zeros((1, 1, 1, D)); q[..., 0] = 10.0
+    k = np.zeros((1, 2, 1, D)); k[0, 0, 0, 0] = 10.0; k[0, 1, 0, 0] = -10.0
+    v = np.zeros((1, 2, 1, D)); v[0, 0, 0, 1] = 1.0; v[0, 1, 0, 2] = 1.0
+    out, lse, probs = ora.attention(q, k, v, softmax_scale=1.0, softcap=1.0)
+    e = math.e
+    np.testing.assert_allclose(probs[0, 0, 0], [e / (e + 1 / e), (1 / e) / (e + 1 / e)], rtol=1e-14)
+    np.testing.assert_allclose(lse[0, 0, 0], math.log(e + 1 / e), rtol=1e-14)
+    np.testing.assert_allclose(out[0, 0, 0, 1:3], probs[0, 0, 0], rtol=1e-14)
+
+
+def test_huge_softcap_is_identity():
+    q, k, v = _rand((1, 11, 2, 16), 21), _rand((1, 11, 2, 16), 22), _rand((1, 11, 2, 16), 23)
+    out, _, _ = ora.attention(q, k, v, 0.25, True, softcap=1e7)
+    np.testing.assert_allclose(out, _sdpa(q, k, v, True, 0.25), atol=1e-10)
+
+
+def test_uniform_and_single_key_and_empty_rows():
+    k, v = _rand((1, 8, 1, 4), 24), _rand((1, 8, 1, 4), 25)
+    q = np.zeros((1, 8, 1, 4))
+    # q = 0: uniform over the visible keys (causal: keys 0..i)
+    out, lse, _ = ora.attention(q, k, v, causal=True)
+    for i in range(8):
+        np.testing.assert_allclose(out[0, i, 0], v[0, :i + 1, 0].mean(0), atol=1e-14)
+        np.testing.assert_allclose(lse[0, 0, i], math.log(i + 1), atol=1e-14)
+    # window (0, 0): every row sees only its own key
+    q2 = _rand((1, 8, 1, 4), 26)
+    out, lse, _ = ora.attention(q2, k, v, 0.5, window_size=(0, 0))
+    np.testing.assert_allclose(out[0, :, 0], v[0, :, 0], atol=1e-14)
+    np.testing.assert_allclose(lse[0, 0], 0.5 * np.einsum("sd,sd->s", q2[0, :, 0], k[0, :, 0]),
+                               atol=1e-14)
+    # causal with negative offset: the first rows see nothing -> out 0, lse -inf
+    out, lse, probs = ora.attention(q2, k, v, causal=True, causal_offset=-3)
+    assert np.all(out[0, :3] == 0) and np.all(np.isneginf(lse[0, 0, :3]))
+    assert np.all(probs[0, 0, :3] == 0)
+
+
+def _brute(q, k, v, scale, causal, window, softcap, slopes, offset):
+    """Pure-Python loops: one score at a time, in the documented pipeline order."""
+    B, Sq, H, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    out = [[[[0.0] * D for _ in range(H)] for _ in range(Sq)] for _ in range(B)]
+    for b in range(B):
+        for h in range(H):
+            kh = h // (H // Hk)
+            for i in range(Sq):
+                qp = i + offset
+                scores = []
+                for j in range(Sk):
+                    ok = (not causal or qp >= j) and (window[0] < 0 or j >= qp - window[0]) \
+                        and (window[1] < 0 or j <= qp + window[1])
+                    if not ok:
+                        continue
+                    s = sum(float(q[b, i, h, d]) * float(k[b, j, kh, d]) for d in range(D)) * scale
+                    if slopes is not None:
+                        s -= float(slopes[b][h]) * abs(qp - j)
+                    if softcap > 0:
+                        s = softcap * math.tanh(s / softcap)
+                    scores.append((j, s))
+                if not scores:
+                    continue
+                m = max(s for _, s in scores)
+                z = sum(math.exp(s - m) for _, s in scores)
+                for d in range(D):
+                    out[b][i][h][d] = sum(math.exp(s - m) / z * float(v[b, j, kh, d]) for j, s in scores)
+    return np.array(out)
+
+
+@pytest.mark.parametrize("case", range(4))
+def test_brute_force_all_features(case):
+    rng = np.random.default_rng(100 + case)
+    B, Sq, Sk, H, Hk, D = 2, [5, 6, 4, 6][case], [5, 4, 7, 6][case], 4, [4, 2, 1, 2][case], 4
+    q, k, v = rng.standard_normal((B, Sq, H, D)), rng.standard_normal((B, Sk, Hk, D)), \
+        rng.standard_normal((B, Sk, Hk, D))
+    causal = case % 2 == 1
+    window = [(-1, -1), (2, 1), (1, -1), (3, 0)][case]
+    softcap = [0.0, 0.7, 2.0, 0.3][case]
+    slopes = rng.random((B, H)) * 0.5
+    offset = [0, 1, 0, 2][case]
+    out, _, _ = ora.attention(q * 1.5, k, v, 0.6, causal, window, softcap, slopes,
+                              causal_offset=offset)
+    ref = _brute(q * 1.5, k, v, 0.6, causal, window, softcap, slopes, offset)
+    np.testing.assert_allclose(out, ref, atol=1e-12)
+
+
+def test_alibi_is_applied_before_softcap():
+    # The two orders disagree on this input; the reference adds ALiBi to the
+    # score before softcap (flash_attn_interface.py:36-42, kernel :308-314).
+    q = np.full((1, 1, 1, 1), 3.0)
+    k = np.array([[[[1.0]], [[1.0]]]])
+    v = np.array([[[[0.0]], [[1.0]]]])
+    slopes = np.array([2.0])
+    out, _, _ = ora.attention(q, k, v, 1.0, False, softcap=1.0, alibi_slopes=slopes,
+                              causal_offset=0)
+    # key 0: |0-0| = 0 -> tanh(3); key 1: |0-1| = 1 -> tanh(3 - 2) = tanh(1)
+    a, b = math.tanh(3.0), math.tanh(1.0)
+    expected = math.exp(b) / (math.exp(a) + math.exp(b))
+    np.testing.assert_allclose(out[0, 0, 0, 0], expected, rtol=1e-14)
+
+
+# ----------------------------------------------------------------- varlen / kv-cache
+def test_varlen_matches_per_sequence_sdpa():
+    # Reference tests/test_compare_implementations.py:140-159.
+    lq, lk = [3, 5], [4, 6]
+    q, k, v = _rand((8, 2, 16), 30), _rand((10, 2, 16), 31), _rand((10, 2, 16), 32)
+    out, lse = ora.attention_varlen(q, k, v, [0, 3, 8], [0, 4, 10], causal=True)
+    exp = np.concatenate([
+        _sdpa(q[None, 0:3], k[None, 0:4], v[None, 0:4], True)[0],
+        _sdpa(q[None, 3:8], k[None, 4:10], v[None, 4:10], True)[0]])
+    np.testing.assert_allclose(out, exp, atol=1e-12)
+    assert lse.shape == (8, 2)
+
+
+def test_varlen_empty_sequences():
+    q, k, v = _rand((5, 1, 4), 33), _rand((3, 1, 4), 34), _rand((3, 1, 4), 35)
+    out, lse = ora.attention_varlen(q, k, v, [0, 0, 5], [0, 3, 3])
+    # second sequence has 5 queries and no keys: zeros and -inf
+    assert np.all(out == 0) and np.all(np.isneginf(lse))
+
+
+def test_paged_gather_is_the_contiguous_sequence():
+    rng = np.random.default_rng(40)
+    page, L = 4, 11
+    contiguous = rng.standard_normal((L, 2, 8))
+    n_pages = 5
+    perm = rng.permutation(n_pages)
+    cache = rng.standard_normal((n_pages, page, 2, 8))
+    for t in range(L):
+        cache[perm[t // page], t % page] = contiguous[t]
+    np.testing.assert_array_equal(ora.gather_paged_kv(cache, perm, L), contiguous)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_kvcache_decode_matches_sdpa_bottom_right(causal):
+    rng = np.random.default_rng(41)
+    page, Sq, Hq, Hk, D = 4, 3, 4, 2, 8
+    lengths = [9, 5]
+    kc = rng.standard_normal((8, page, Hk, D))
+    vc = rng.standard_normal((8, page, Hk, D))
+    bt = np.array([[3, 0, 6], [5, 1, 2]])
+    q = rng.standard_normal((2, Sq, Hq, D))
+    out, _, _, _ = ora.attention_kvcache(q, kc, vc, cache_seqlens=lengths, block_table=bt,
+                                         causal=causal)
+    for b, L in enumerate(lengths):
+        kb = ora.gather_paged_kv(kc, bt[b], L)[None]
+        vb = ora.gather_paged_kv(vc, bt[b], L)[None]
+        mask = torch.ones(Sq, L, dtype=torch.bool).tril(diagonal=L - Sq) if causal else None
+        exp = _sdpa(q[b:b + 1], kb, vb, mask=mask, gqa=True, scale=1 / math.sqrt(D))
+        np.testing.assert_allclose(out[b:b + 1], exp, atol=1e-12)
+
+
+def test_kvcache_append_then_attend():
+    rng = np.random.default_rng(42)
+    kc = rng.standard_normal((2, 10, 1, 4))
+    vc = rng.standard_normal((2, 10, 1, 4))
+    kn, vn = rng.standard_normal((2, 2, 1, 4)), rng.standard_normal((2, 2, 1, 4))
+    q = rng.standard_normal((2, 2, 1, 4))
+    out, _, kc2, vc2 = ora.attention_kvcache(q, kc, vc, cache_seqlens=[3, 7], k_new=kn, v_new=vn,
+                                             causal=True)
+    np.testing.assert_array_equal(kc2[0, 3:5], kn[0])
+    np.testing.assert_array_equal(kc2[1, 7:9], kn[1])
+    np.testing.assert_array_equal(vc2[1, 7:9], vn[1])
+    np.testing.assert_array_equal(kc2[0, :3], kc[0, :3])
+    exp = _sdpa(q[:1], kc2[:1, :5], vc2[:1, :5],
+                mask=torch.ones(2, 5, dtype=torch.bool).tril(diagonal=3))
+    np.testing.assert_allclose(out[:1], exp, atol=1e-12)
+
+
+@pytest.mark.parametrize("interleaved", [True, False])
+def test_rotary_is_a_complex_rotation(interleaved):
+    rng = np.random.default_rng(43)
+    S, H, D, R = 5, 2, 8, 6
+    x = rng.standard_normal((S, H, D))
+    theta = rng.standard_normal((10, R // 2))
+    pos = np.array([0, 3, 9, 4, 1])
+    out = ora.apply_rotary(x, np.cos(theta), np.sin(theta), pos, interleaved)
+    if interleaved:
+        z = x[..., 0:R:2] + 1j * x[..., 1:R:2]
+    else:
+        z = x[..., :R // 2] + 1j * x[..., R // 2:R]
+    zr = z * np.exp(1j * theta[pos])[:, None, :]
+    if interleaved:
+        np.testing.assert_allclose(out[..., 0:R:2], zr.real, atol=1e-14)
+        np.testing.assert_allclose(out[..., 1:R:2], zr.imag, atol=1e-14)
+    else:
+        np.testing.assert_allclose(out[..., :R // 2], zr.real, atol=1e-14)
+        np.testing.assert_allclose(out[..., R // 2:R], zr.imag, atol=1e-14)
+    np.testing.assert_array_equal(out[..., R:], x[..., R:])
+
+
+# ----------------------------------------------------------------- quantizer
+def _f32(x: Fraction) -> Fraction:
+    """Round an exact rational to the nearest binary32 value (ties to even)."""
+    if x == 0:
+        return Fraction(0)
+    sign = -1 if x < 0 else 1
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -126)
+    ulp = Fraction(2) ** (e - 23)
+    n = a / ulp
+    fl = n.numerator // n.denominator
+    rem = n - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return sign * fl * ulp
+
+
+def _exact_quant_row(row, divide: bool):
+    """Quantizer on exact rationals with explicit binary32 rounding after each op."""
+    vals = [Fraction(float(x)) for x in row]
+    amax = max(abs(x) for x in vals)
+    s = _f32(max(amax, Fraction(1)) / 127)
+    inv = _f32(1 / s)
+    out = []
+    for x in vals:
+        y = _f32(x / s) if divide else _f32(x * inv)
+        if y >= 0:
+            t = _f32(y + Fraction(1, 2))
+            r = t.numerator // t.denominator
+        else:
+            t = _f32(y - Fraction(1, 2))
+            r = -((-t.numerator) // t.denominator)
+        out.append(int(r))
+    return out, float(s)
+
+
+def _known_rows(D=32):
+    rng = np.random.default_rng(50)
+    rows = [np.zeros(D), np.linspace(-0.9, 0.9, D), rng.standard_normal(D),
+            rng.standard_normal(D) * 8.0, np.full(D, 1.0), rng.standard_normal(D) * 300.0]
+    tie = np.zeros(D)
+    tie[0], tie[1], tie[2], tie[3] = 127.0, 0.5, -0.5, 2.5     # s = 1 exactly: x.5 ties
+    rows.append(tie)
+    return np.stack(rows).astype(np.float16)
+
+
+def test_round_half_away_known_answers():
+    x = np.array([0.5, -0.5, 1.5, 2.5, -2.5, 0.49999997, -0.49999997, 0.0, 126.5], np.float32)
+    got = quant.round_half_away(x)
+    # 0.49999997 + 0.5 rounds to 1.0 in binary32 (ties-to-even), so floor gives 1.
+    np.testing.assert_array_equal(got, [1, -1, 2, 3, -3, 1, -1, 0, 127])
+
+
+@pytest.mark.parametrize("divide", [False, True])
+def test_quantizer_matches_exact_arithmetic(divide):
+    rows = _known_rows()
+    q8, s = (quant.quantize_q_rows if divide else quant.quantize_k_rows)(rows)
+    for r, row in enumerate(rows):
+        exp8, exp_s = _exact_quant_row(row, divide)
+        assert q8[r].tolist() == exp8, f"row {r}"
+        assert float(s[r]) == exp_s
+    # known values: zero row -> scale 1/127, all zeros; the tie row has s = 1
+    assert np.all(q8[0] == 0) and s[0] == np.float32(1.0) / np.float32(127.0)
+    assert s[6] == 1.0 and q8[6][:4].tolist() == [127, 1, -1, 3]
+
+
+def _c_oracle():
+    lib = os.path.join(ROOT, "oracle", "libfa_oracle.so")
+    if not os.path.exists(lib):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "oracle")], check=True,
+                       capture_output=True)
+    c = ctypes.CDLL(lib)
+    for name in ("oracle_quantize_k_rows_f16", "oracle_quantize_q_rows_f16"):
+        getattr(c, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                     ctypes.c_int64, ctypes.c_int64]
+    return c
+
+
+@pytest.mark.parametrize("divide", [False, True])
+def test_numpy_and_c_quantizers_agree(divide):
+    rng = np.random.default_rng(51)
+    x = (rng.standard_normal((4000, 128)) * rng.choice([0.3, 1, 8, 100], (4000, 1))).astype(np.float16)
+    x[:10] = _known_rows(128)[:7].repeat(2, axis=0)[:10]
+    c = _c_oracle()
+    k8 = np.empty(x.shape, np.int8)
+    s = np.empty(x.shape[0], np.float32)
+    fn = c.oracle_quantize_q_rows_f16 if divide else c.oracle_quantize_k_rows_f16
+    fn(x.ctypes.data, k8.ctypes.data, s.ctypes.data, x.shape[0], x.shape[1])
+    n8, ns = (quant.quantize_q_rows if divide else quant.quantize_k_rows)(x)
+    np.testing.assert_array_equal(k8, n8)
+    np.testing.assert_array_equal(s.view(np.uint32), ns.view(np.uint32))
+
+
+def test_quantized_values_are_bounded_and_close():
+    x = (np.random.default_rng(52).standard_normal((500, 64)) * 5).astype(np.float16)
+    k8, s = quant.quantize_k_rows(x)
+    assert np.abs(k8.astype(int)).max() <= 127
+    err = np.abs(k8 * s[:, None].astype(np.float64) - x.astype(np.float64))
+    assert np.all(err <= s[:, None] * 0.5 * (1 + 1e-6))
+
+
+def test_int8_attention_exact_when_quantization_is_lossless():
+    # Integer-valued rows with amax 127 quantize with s = 1 exactly, so the INT8
+    # oracle equals the float attention oracle on the same inputs.
+    rng = np.random.default_rng(53)
+    B, H, S, D = 1, 2, 8, 32
+    q = rng.integers(-127, 128, (B, H, S, D)).astype(np.float16)
+    k = rng.integers(-127, 128, (B, H, S, D)).astype(np.float16)
+    q[..., 0] = 127
+    k[..., 0] = -127
+    v = rng.standard_normal((B, H, S, D))
+    for causal in (False, True):
+        o8, l8 = quant.attention_int8(q, k, v, causal, sm_scale=1e-3)
+        of, lf, _ = ora.attention(q.transpose(0, 2, 1, 3), k.transpose(0, 2, 1, 3),
+                                  v.transpose(0, 2, 1, 3), 1e-3, causal)
+        np.testing.assert_allclose(o8, of.transpose(0, 2, 1, 3), atol=1e-12)
+        np.testing.assert_allclose(l8, lf, atol=1e-12)
