@@ -99,7 +99,11 @@ def test_alibi(per_batch):
 
 @pytest.mark.parametrize("softcap", [30.0, 1.0, 0.05])
 def test_softcap(softcap):
-    q, k, v = (randn((2, 160, 2, 128), s, scale=2.0) for s in (51, 52, 53))
+    # q and k at 2x N(0,1) push scores into the cap; v stays N(0,1): with 2x
+    # values the outputs reach [4, 8), where one fp16 ulp (3.9e-3) is already
+    # above the 2e-3 bar.
+    q, k = (randn((2, 160, 2, 128), s, scale=2.0) for s in (51, 52))
+    v = randn((2, 160, 2, 128), 53)
     _check(q, k, v, causal=True, softcap=softcap)
 
 
