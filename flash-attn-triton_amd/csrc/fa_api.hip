@@ -35,6 +35,15 @@ int hip_status(hipError_t e, const char* what) {
   return fail(FA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Positions are 32-bit inside the kernels: lengths and the query position
+// offset stay within 2^29 and windows are clamped to 2^30 - 1, which is
+// unbounded at those lengths, so qpos +- window never overflows.
+constexpr int64_t kMaxLen = int64_t(1) << 29;
+int clamp_window(int64_t w) {
+  const int64_t cap = (int64_t(1) << 30) - 1;
+  return w < 0 ? -1 : (int)(w > cap ? cap : w);
+}
+
 bool supported_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 
 // 16-byte vector loads need 16-byte aligned rows: base pointer aligned and
@@ -56,6 +65,7 @@ void fill_scale(fa::FwdParams& p, float scale, float softcap, const float* alibi
   p.scale = scale;
   p.scale_log2 = scale * fa::kLog2e;
   p.softcap = softcap;
+  p.softcap_k = softcap > 0.f ? 2.f * fa::kLog2e / softcap : 0.f;
   p.alibi = alibi;
 }
 
@@ -143,8 +153,9 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
     return fail(FA_ERR_INVALID, "fa_fwd_dense: bad sizes B=%lld Sq=%lld Sk=%lld Hq=%lld Hk=%lld",
                 (long long)batch, (long long)seqlen_q, (long long)seqlen_k, (long long)heads_q,
                 (long long)heads_k);
-  if (seqlen_q > INT32_MAX / 2 || seqlen_k > INT32_MAX / 2 || batch * heads_q > INT32_MAX)
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: sizes exceed 32-bit indexing");
+  if (seqlen_q > kMaxLen || seqlen_k > kMaxLen || q_pos_offset > kMaxLen ||
+      q_pos_offset < -kMaxLen || batch * heads_q > INT32_MAX)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: sizes or position offset exceed 2^29");
   if (!aligned16(q, q_stride, 3) || !aligned16(k, k_stride, 3) || !aligned16(v, v_stride, 3) ||
       !aligned16(out, o_stride, 3))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: tensors must be 16-byte aligned with strides "
@@ -162,8 +173,8 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
   fill_scale(p, softmax_scale, softcap, alibi_slopes);
   p.alibi_sb = alibi_batch_stride;
   p.causal = causal != 0;
-  p.window_left = window_left < 0 ? -1 : (int)(window_left > INT32_MAX / 4 ? INT32_MAX / 4 : window_left);
-  p.window_right = window_right < 0 ? -1 : (int)(window_right > INT32_MAX / 4 ? INT32_MAX / 4 : window_right);
+  p.window_left = clamp_window(window_left);
+  p.window_right = clamp_window(window_right);
   p.q_offset = q_pos_offset;
   p.num_splits = 1;
   p.heavy_first = p.causal || p.window_right >= 0;
@@ -192,8 +203,8 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
   if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || heads_q <= 0 || heads_k <= 0 ||
       heads_q % heads_k != 0)
     return fail(FA_ERR_INVALID, "fa_fwd_varlen: bad sizes");
-  if (max_seqlen_q > INT32_MAX / 2 || batch * heads_q > INT32_MAX)
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: sizes exceed 32-bit indexing");
+  if (max_seqlen_q > kMaxLen || max_seqlen_k > kMaxLen || batch * heads_q > INT32_MAX)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: sizes exceed 2^29");
   if (!aligned16(q, q_stride, 2) || !aligned16(k, k_stride, 2) || !aligned16(v, v_stride, 2) ||
       !aligned16(out, o_stride, 2))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: tensors must be 16-byte aligned with strides "
@@ -212,8 +223,8 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
   fill_scale(p, softmax_scale, softcap, alibi_slopes);
   p.alibi_sb = alibi_batch_stride;
   p.causal = causal != 0;
-  p.window_left = window_left < 0 ? -1 : (int)(window_left > INT32_MAX / 4 ? INT32_MAX / 4 : window_left);
-  p.window_right = window_right < 0 ? -1 : (int)(window_right > INT32_MAX / 4 ? INT32_MAX / 4 : window_right);
+  p.window_left = clamp_window(window_left);
+  p.window_right = clamp_window(window_right);
   p.num_splits = 1;
   p.heavy_first = p.causal || p.window_right >= 0;
   return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim, needs_generic(p),
@@ -264,8 +275,8 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: bad sizes");
   if (block_table && page_size <= 0)
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: page_size must be positive");
-  if (seqlen_q * (heads_q / heads_k) > INT32_MAX / 2 || max_keys > INT32_MAX / 2)
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: sizes exceed 32-bit indexing");
+  if (seqlen_q * (heads_q / heads_k) > kMaxLen || max_keys > kMaxLen)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: sizes exceed 2^29");
   if (!aligned16(q, q_stride, 3) || !aligned16(k_cache, k_cache_stride, 3) ||
       !aligned16(v_cache, v_cache_stride, 3) || !aligned16(out, o_stride, 3))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: tensors must be 16-byte aligned with "
@@ -293,8 +304,8 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
   p.alibi_sb = alibi_batch_stride;
   p.causal = causal != 0;
   p.kv_causal_offset = causal != 0;
-  p.window_left = window_left < 0 ? -1 : (int)(window_left > INT32_MAX / 4 ? INT32_MAX / 4 : window_left);
-  p.window_right = window_right < 0 ? -1 : (int)(window_right > INT32_MAX / 4 ? INT32_MAX / 4 : window_right);
+  p.window_left = clamp_window(window_left);
+  p.window_right = clamp_window(window_right);
   p.seqlens_k = cache_seqlens;
   p.block_table = block_table; p.bt_stride = block_table_stride; p.page_size = (int)page_size;
   p.cache_rows = cache_batch_idx; p.leftpad = cache_leftpad;

@@ -30,6 +30,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 // conversion wrappers reinterpret them.
 struct F16 {
   static constexpr int kBytes = 2;
+  // Row sums may be taken over the rounded P: fp16 rounding (2^-12 relative)
+  // keeps the log-sum-exp within 3e-4.
+  static constexpr bool kSumRounded = true;
   __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                    __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
@@ -42,10 +45,18 @@ struct F16 {
   __device__ static inline float to_float(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
   }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_f16 against (1, 1)).
+  __device__ static inline float sum2(uint32_t pk, float acc) {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk), one, acc, false);
+  }
 };
 
 struct BF16 {
   static constexpr int kBytes = 2;
+  // bf16 rounding (2^-9 relative) would move the log-sum-exp of short rows by
+  // up to 2e-3: row sums are taken over the fp32 P instead.
+  static constexpr bool kSumRounded = false;
   __device__ static inline f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                     __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -57,6 +68,11 @@ struct BF16 {
   }
   __device__ static inline float to_float(uint16_t h) {
     return __builtin_bit_cast(float, (uint32_t)h << 16);
+  }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_bf16 against (1, 1)).
+  __device__ static inline float sum2(uint32_t pk, float acc) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), one, acc, false);
   }
 };
 
@@ -84,5 +100,28 @@ __device__ inline int xcd_remap(int L, int total) {
 
 __device__ inline u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Raw buffer addressing.  A buffer resource covers [base, base + num_bytes);
+// a raw buffer load whose byte offset lies at or beyond num_bytes returns zero
+// without touching memory, so tiles that run past the end of a sequence need
+// no branch.  Word 3 is the gfx9-family raw-buffer configuration (32-bit
+// dwords, no swizzle).  The base and size must be wave-uniform: they live in
+// scalar registers.
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t num_bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)num_bytes,
+                                           0x00020000);
+}
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Byte extent of rows [row0, rows) of a strided 2-byte tensor whose rows hold
+// `row_elems` elements at `row_stride` elements apart, clamped to 32 bits;
+// zero when no row is left.
+__device__ inline uint32_t rows_extent(int row0, int rows, int64_t row_stride, int row_elems) {
+  if (row0 >= rows) return 0;
+  const int64_t bytes = ((int64_t)(rows - 1 - row0) * row_stride + row_elems) * 2;
+  return bytes > 0xffffffffll ? 0xffffffffu : (uint32_t)bytes;
+}
 
 }  // namespace fa

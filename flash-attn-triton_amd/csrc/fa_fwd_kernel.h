@@ -50,7 +50,7 @@ struct FwdParams {
   int64_t o_sb, o_ss, o_sh;
   int64_t lse_sb, lse_ss, lse_sh;
   int batch, seqlen_q, seqlen_k, heads_q, heads_k, group;
-  float scale, scale_log2, softcap;
+  float scale, scale_log2, softcap, softcap_k;   // softcap_k = 2 log2(e) / softcap
   const float* alibi; int64_t alibi_sb;
   int causal, window_left, window_right;
   int64_t q_offset;

@@ -3,7 +3,7 @@
 // fa_fwd_bf16.hip) so the two halves compile in parallel.
 #pragma once
 
-#include "fa_fwd_kernel.h"
+#include "fa_prefill_kernel.h"
 
 namespace fa {
 
@@ -36,11 +36,40 @@ hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipS
   return hipGetLastError();
 }
 
+// Prefill kernel tiles (fa_prefill_kernel.h) per head dim: 4 waves x 32 rows;
+// 64-key tiles, 32 at D=256 (register budget of the O^T accumulators).
+template <int D> struct PrefillCfg2 { static constexpr int NW = 4, BN = D >= 256 ? 32 : 64; };
+
+template <class T, int D, int NW, int BN, bool GEN>
+hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
+  using Tile = PrefillTile<D, NW, BN>;
+  auto kern = prefill_kernel<T, D, NW, BN, GEN>;
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    lds_attr_set = true;
+  }
+  p.n_mblocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
+  const int64_t total = (int64_t)p.n_mblocks * p.heads_q * p.batch;
+  if (total <= 0) return hipSuccess;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+  p.total_blocks = (int)total;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  return hipGetLastError();
+}
+
 template <class T, int D, int MODE, bool GEN>
 hipError_t launch_fwd_d(const FwdParams& p, hipStream_t st) {
   if (MODE == kModePrefill) {
-    using C = PrefillCfg<D>;
-    return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, p.seqlen_q, p.heads_q * p.batch, st);
+    if constexpr (D % 32 == 0) {
+      using C = PrefillCfg2<D>;
+      return launch_prefill_cfg<T, D, C::NW, C::BN, GEN>(p, st);
+    } else {
+      using C = PrefillCfg<D>;
+      return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, p.seqlen_q, p.heads_q * p.batch, st);
+    }
   }
   const int rows = p.seqlen_q * p.group;
   const int outer = p.heads_k * p.batch * p.num_splits;

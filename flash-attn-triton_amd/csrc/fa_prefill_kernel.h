@@ -1,0 +1,362 @@
+// FlashAttention-2 prefill forward for gfx950 (dense, cross and varlen), fp16 / bf16.
+//
+// Same semantics as fwd_kernel (fa_fwd_kernel.h), which it replaces for
+// prefill at head dims that are multiples of 32; the behaviour follows the
+// reference's dense and varlen forward kernels
+// (/root/reference/flash_attn_triton/triton_kernel/attention_kernel.py:424-533,
+// :275-372, :27-104).  What differs is the schedule:
+//
+// * K and V tiles are read with raw buffer loads whose resource ends at the
+//   last valid key row of the (batch, head) slab: rows past the sequence come
+//   back as zeros, so the loads carry no branch and no 64-bit address math.
+//   Every thread's byte offsets are computed once; per tile only the scalar
+//   base of the resource moves.
+// * fp16 row sums are taken from the packed P operand with v_dot2 against
+//   (1, 1): numerator (P V) and denominator (sum P) see the same rounded P,
+//   at half the adds.  bf16 sums the fp32 P (its rounding is 8x coarser).
+// * The running max is raised lazily: a row's max is only moved when a tile
+//   exceeds it by more than kRescaleSlack (log2 units).  Until then
+//   exp2(s - m) stays below 2^kRescaleSlack, which fp16/bf16 P and the fp32
+//   accumulators hold exactly as well, and the whole-wave O^T rescale
+//   (D/2 multiplies per lane) is skipped for the tile.  The final result is
+//   normalized by the same sum, so it does not depend on when m moved.
+//
+// Layout per workgroup (NW waves, BM = 32*NW query rows, BN keys per tile):
+//   S^T = K Q^T on v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q^T in VGPRs),
+//   O^T += V^T P^T (A = V^T from an LDS copy stored transposed, B = P^T from the
+//   score accumulators), K/V double-buffered in LDS, one barrier per tile.
+#pragma once
+
+#include "fa_fwd_kernel.h"
+
+namespace fa {
+
+constexpr float kRescaleSlack = 8.0f;
+
+template <int D, int NW, int BN>
+struct PrefillTile {
+  static constexpr int BM = NW * 32;
+  static constexpr int NT = NW * 64;
+  static constexpr int KSTR = D + 8;     // K row pitch in LDS (elements): 16 B pad
+  static constexpr int VSTR = BN + 4;    // V^T row pitch in LDS (elements): 8 B pad
+  static constexpr int KTILE = BN * KSTR;
+  static constexpr int VTILE = D * VSTR;
+  static constexpr int LDS_BYTES = 2 * (KTILE + VTILE) * 2;
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int KPT = BN * CPR / NT;         // K chunks per thread per tile
+  static constexpr int VGR = (BN / 4) * CPR;        // (4 keys x 8 dims) V groups per tile
+  static constexpr int VPT = (VGR + NT - 1) / NT;   // V groups per thread per tile
+  static_assert(D % 32 == 0, "head dim must be a multiple of 32");
+  static_assert(BN % 32 == 0, "tile must hold whole 32-key MFMA blocks");
+  static_assert((BN * CPR) % NT == 0 && NT % CPR == 0, "K tile must split evenly over threads");
+  static_assert(VGR <= NT || VGR % NT == 0, "V tile must split evenly over threads");
+};
+
+template <class T, int D, int NW, int BN, bool GENERIC>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_kernel(const FwdParams p) {
+  using Tile = PrefillTile<D, NW, BN>;
+  constexpr int BM = Tile::BM;
+  constexpr int NT = Tile::NT;
+  constexpr int KSTR = Tile::KSTR;
+  constexpr int VSTR = Tile::VSTR;
+  constexpr int KTILE = Tile::KTILE;
+  constexpr int VTILE = Tile::VTILE;
+  constexpr int CPR = Tile::CPR;
+  constexpr int KPT = Tile::KPT;
+  constexpr int VGR = Tile::VGR;
+  constexpr int VPT = Tile::VPT;
+  constexpr int NKC = D / 16;      // 16-dim MFMA k-steps for S^T
+  constexpr int NDB = D / 32;      // 32-dim output blocks of O^T
+  constexpr int NKB = BN / 32;     // 32-key blocks per tile
+  constexpr int NCC = BN / 16;     // 16-key k-steps for O^T
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
+  const int c32 = lane & 31;
+  const int g = lane >> 5;
+
+  // ------------------------------------------------------------ work item
+  int id = xcd_remap(blockIdx.x, p.total_blocks);
+  int mb = id % p.n_mblocks;
+  id /= p.n_mblocks;
+  const int hh = id % p.heads_q;
+  const int b = id / p.heads_q;
+  if (p.heavy_first) mb = p.n_mblocks - 1 - mb;
+  const int kvh = hh / p.group;
+
+  int Sq, Sk;
+  int64_t q_base, o_base, lse_base, k_base, v_base;
+  if (p.cu_q != nullptr) {
+    const int qs = p.cu_q[b], ks = p.cu_k[b];
+    Sq = p.cu_q[b + 1] - qs;
+    Sk = p.cu_k[b + 1] - ks;
+    q_base = (int64_t)qs * p.q_ss;
+    o_base = (int64_t)qs * p.o_ss;
+    lse_base = (int64_t)qs * p.lse_ss;
+    k_base = (int64_t)ks * p.k_ss;
+    v_base = (int64_t)ks * p.v_ss;
+  } else {
+    Sq = p.seqlen_q;
+    Sk = p.seqlen_k;
+    q_base = (int64_t)b * p.q_sb;
+    o_base = (int64_t)b * p.o_sb;
+    lse_base = (int64_t)b * p.lse_sb;
+    k_base = (int64_t)b * p.k_sb;
+    v_base = (int64_t)b * p.v_sb;
+  }
+  q_base += (int64_t)hh * p.q_sh;
+  o_base += (int64_t)hh * p.o_sh;
+  lse_base += (int64_t)hh * p.lse_sh;
+  k_base += (int64_t)kvh * p.k_sh;
+  v_base += (int64_t)kvh * p.v_sh;
+  const int64_t qoff = p.q_offset;
+
+  const int row0 = mb * BM;
+  if (row0 >= Sq) return;   // varlen blocks past this sequence's queries
+  const int row_last = min(row0 + BM, Sq) - 1;
+
+  const int qi = row0 + w * 32 + c32;
+  const bool row_valid = qi < Sq;
+  const int qpos = qi + (int)qoff;
+  float slope = 0.f;
+  if (GENERIC && p.alibi != nullptr && row_valid) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
+
+  const int wrow0 = row0 + w * 32;
+  const bool wave_active = wrow0 <= row_last;
+  // Positions fit in 32 bits (the host keeps lengths and offsets below 2^29).
+  const int qoff32 = (int)qoff;
+  const int qpos_w_min = wrow0 + qoff32;
+  const int qpos_w_max = min(wrow0 + 31, row_last) + qoff32;
+
+  const int wl = p.window_left, wr = p.window_right;
+  const bool causal = p.causal != 0;
+  // Keys this row may see on a masked tile: [key_lo, key_hi].
+  const int qp32 = qpos;
+  int key_hi = Sk - 1;
+  if (causal) key_hi = min(key_hi, qp32);
+  if (wr >= 0) key_hi = min(key_hi, qp32 + wr);
+  const int key_lo = wl >= 0 ? qp32 - wl : INT32_MIN;
+
+  // Key range [k_lo, k_hi) any row of the workgroup can see.
+  int k_hi = Sk;
+  if (causal) k_hi = min(k_hi, row_last + qoff32 + 1);
+  if (wr >= 0) k_hi = min(k_hi, row_last + qoff32 + wr + 1);
+  int k_lo = 0;
+  if (wl >= 0) k_lo = max(0, row0 + qoff32 - wl);
+  const int t_begin = k_lo / BN;
+  const int t_end = k_hi > k_lo ? (k_hi + BN - 1) / BN : t_begin;
+
+  // ------------------------------------------------------------ Q^T in VGPRs
+  const uint16_t* qg = static_cast<const uint16_t*>(p.q);
+  u32x4 qreg[NKC];
+  {
+    const uint16_t* qrow = qg + q_base + (int64_t)qi * p.q_ss;
+#pragma unroll
+    for (int kc = 0; kc < NKC; ++kc)
+      qreg[kc] = row_valid ? load16(qrow + kc * 16 + g * 8) : u32x4{0, 0, 0, 0};
+    // Retire the Q loads here: otherwise the loop's first use of qreg has to
+    // assume they may still be in flight behind the tile prefetches and waits
+    // for every outstanding load.
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0)
+  }
+
+  // ------------------------------------------------------------ tile loads
+  // K: chunk c = tid + i*NT of the tile is row c / CPR, 16-byte column c % CPR.
+  // V: group gi = tid + i*NT holds keys 4*(gi / CPR) + u (u < 4), column gi % CPR.
+  const uint16_t* kg = static_cast<const uint16_t*>(p.k) + k_base;
+  const uint16_t* vg = static_cast<const uint16_t*>(p.v) + v_base;
+  // Every byte offset goes into the VGPR offset operand: the range check of a
+  // raw buffer load covers that operand but not the scalar one.
+  const uint32_t k_row_b = (uint32_t)(p.k_ss * 2);
+  const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
+  const bool v_owner = VPT * NT == VGR || tid < VGR;   // threads past VGR own no V group
+  uint32_t k_off[KPT], v_off[VPT][4];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int c = tid + i * NT;
+    k_off[i] = (uint32_t)(c / CPR) * k_row_b + (uint32_t)(c % CPR) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int gi = tid % VGR + i * NT;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      v_off[i][u] = (uint32_t)((gi / CPR) * 4 + u) * v_row_b + (uint32_t)(gi % CPR) * 16;
+  }
+
+  u32x4 kreg[KPT];
+  u32x4 vreg[VPT][4];
+  auto load_tile = [&](int t) {
+    const int n0 = t * BN;
+    const auto krs = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
+    const auto vrs = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) kreg[i] = buf_load16(krs, k_off[i], 0);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        vreg[i][u] = v_owner ? buf_load16(vrs, v_off[i][u], 0) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* Ks = smem + buf * (KTILE + VTILE);
+    uint16_t* Vt = Ks + KTILE;
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int c = tid + i * NT;
+      store16(Ks + (c / CPR) * KSTR + (c % CPR) * 8, kreg[i]);
+    }
+    if (v_owner) {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const int gi = tid % VGR + i * NT;
+        const int ng = gi / CPR, d0 = (gi % CPR) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+          const int wd = e >> 1;
+          u32x2 pr;
+          pr[0] = __builtin_amdgcn_perm(vreg[i][1][wd], vreg[i][0][wd], sel);
+          pr[1] = __builtin_amdgcn_perm(vreg[i][3][wd], vreg[i][2][wd], sel);
+          *reinterpret_cast<u32x2*>(Vt + (d0 + e) * VSTR + ng * 4) = pr;
+        }
+      }
+    }
+  };
+
+  // ------------------------------------------------------------ main loop
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+  float m_run = -INFINITY;   // running (possibly stale) max, log2 units
+  float l_run = 0.f;         // this lane's partial row sum
+
+  if (t_begin < t_end) {
+    load_tile(t_begin);
+    store_tile(0);
+  }
+  for (int t = t_begin; t < t_end; ++t) {
+    const int buf = (t - t_begin) & 1;
+    __syncthreads();
+    const bool has_next = t + 1 < t_end;
+    if (has_next) load_tile(t + 1);
+
+    const int n0 = t * BN;
+    const int n1 = n0 + BN;   // exclusive
+    bool skip = !wave_active || n0 >= Sk;
+    if (causal) skip = skip || n0 > qpos_w_max;
+    if (wr >= 0) skip = skip || n0 > qpos_w_max + wr;
+    if (wl >= 0) skip = skip || n1 - 1 < qpos_w_min - wl;
+    if (!skip) {
+      bool need_mask = n1 > Sk;
+      if (causal) need_mask = need_mask || n1 - 1 > qpos_w_min;
+      if (wr >= 0) need_mask = need_mask || n1 - 1 > qpos_w_min + wr;
+      if (wl >= 0) need_mask = need_mask || n0 < qpos_w_max - wl;
+
+      const uint16_t* Ks = smem + buf * (KTILE + VTILE);
+      const uint16_t* Vt = Ks + KTILE;
+
+      f32x16 s[NKB];
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        s[kb] = f32x16{};
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+          const u32x4 a = load16(Ks + (kb * 32 + c32) * KSTR + kc * 16 + g * 8);
+          s[kb] = T::mfma32(a, qreg[kc], s[kb]);
+        }
+      }
+
+      // Scores -> log2 units (GENERIC applies ALiBi and softcap first), mask.
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+          float x = s[kb][v];
+          if (GENERIC) {
+            x *= p.scale;
+            if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qp32 - key)), x);
+            if (p.softcap > 0.f) {
+              // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
+              const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
+              x = p.softcap - 2.f * p.softcap * __builtin_amdgcn_rcpf(1.f + e2);
+            }
+            x *= kLog2e;
+          }
+          if (need_mask && (key < key_lo || key > key_hi)) x = -INFINITY;
+          s[kb][v] = x;
+          mx = fmaxf(mx, x);
+        }
+      }
+      // Non-generic scores stay raw (scale > 0): the scale is folded into the
+      // exp2 argument below, and into the max here.
+      const float sl = GENERIC ? 1.f : p.scale_log2;
+      mx = halves_max(mx) * sl;
+      const bool raise = mx > m_run + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(raise)) {
+        const float m_new = raise ? mx : m_run;
+        const float alpha = m_new == m_run ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+
+#pragma unroll
+      for (int cc = 0; cc < NCC; ++cc) {
+        f32x16& sv = s[cc >> 1];
+        const int o8 = (cc & 1) * 8;
+        u32x4 pb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
+          pb[j] = T::pack2(e0, e1);
+          if (T::kSumRounded)
+            l_run = T::sum2(pb[j], l_run);
+          else
+            l_run += e0 + e1;
+        }
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const uint16_t* vrow = Vt + (db * 32 + c32) * VSTR + cc * 16 + g * 4;
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+          const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+          acc[db] = T::mfma32(a, pb, acc[db]);
+        }
+      }
+    }
+    if (has_next) store_tile(buf ^ 1);
+  }
+
+  // ------------------------------------------------------------ epilogue
+  const float l_tot = halves_sum(l_run);
+  const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float lse_val = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+  if (!row_valid) return;
+
+  uint16_t* orow = static_cast<uint16_t*>(p.o) + o_base + (int64_t)qi * p.o_ss;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = db * 32 + r * 8 + g * 4;
+      u32x2 val;
+      val[0] = T::pack2(acc[db][4 * r] * inv_l, acc[db][4 * r + 1] * inv_l);
+      val[1] = T::pack2(acc[db][4 * r + 2] * inv_l, acc[db][4 * r + 3] * inv_l);
+      *reinterpret_cast<u32x2*>(orow + d) = val;
+    }
+  }
+  if (p.lse != nullptr && g == 0) p.lse[lse_base + (int64_t)qi * p.lse_ss] = lse_val;
+}
+
+}  // namespace fa
