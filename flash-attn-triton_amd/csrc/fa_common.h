@@ -101,6 +101,16 @@ __device__ inline int xcd_remap(int L, int total) {
 __device__ inline u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
+// gfx950 LDS transpose read (ds_read_b64_tr_b16).  Every lane names 8 bytes
+// (4 consecutive 16-bit elements) of LDS; within each group of 16 lanes the
+// reads form a 4 x 16 block whose row r is supplied by lanes 4r..4r+3, and
+// lane i of the group receives column i of that block (rows 0..3).
+typedef short s16x4v __attribute__((__vector_size__(4 * sizeof(short))));
+__device__ inline u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((address_space(3))) s16x4v lds_s16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)p));
+}
+
 // Raw buffer addressing.  A buffer resource covers [base, base + num_bytes);
 // a raw buffer load whose byte offset lies at or beyond num_bytes returns zero
 // without touching memory, so tiles that run past the end of a sequence need

@@ -23,8 +23,9 @@
 //
 // Layout per workgroup (NW waves, BM = 32*NW query rows, BN keys per tile):
 //   S^T = K Q^T on v_mfma_f32_32x32x16 (A = K rows from LDS, B = Q^T in VGPRs),
-//   O^T += V^T P^T (A = V^T from an LDS copy stored transposed, B = P^T from the
-//   score accumulators), K/V double-buffered in LDS, one barrier per tile.
+//   O^T += V^T P^T (A = V^T gathered from the row-major V tile with the gfx950
+//   LDS transpose read ds_read_b64_tr_b16, B = P^T from the score
+//   accumulators), K/V double-buffered in LDS, one barrier per tile.
 #pragma once
 
 #include "fa_fwd_kernel.h"
@@ -37,19 +38,21 @@ template <int D, int NW, int BN>
 struct PrefillTile {
   static constexpr int BM = NW * 32;
   static constexpr int NT = NW * 64;
-  static constexpr int KSTR = D + 8;     // K row pitch in LDS (elements): 16 B pad
-  static constexpr int VSTR = BN + 4;    // V^T row pitch in LDS (elements): 8 B pad
+  // Row pitches in LDS (elements).  K rows carry 16 B of padding: the 16 rows
+  // a ds_read_b128 quarter-wave touches start on distinct 16-byte bank groups.
+  // V rows carry 64 B: the four rows one transpose read covers per 16-lane
+  // group (and the two column halves of a 32-lane group) land on distinct
+  // banks.
+  static constexpr int KSTR = D + 8;
+  static constexpr int VSTR = D + 32;
   static constexpr int KTILE = BN * KSTR;
-  static constexpr int VTILE = D * VSTR;
+  static constexpr int VTILE = BN * VSTR;
   static constexpr int LDS_BYTES = 2 * (KTILE + VTILE) * 2;
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int KPT = BN * CPR / NT;         // K chunks per thread per tile
-  static constexpr int VGR = (BN / 4) * CPR;        // (4 keys x 8 dims) V groups per tile
-  static constexpr int VPT = (VGR + NT - 1) / NT;   // V groups per thread per tile
+  static constexpr int KPT = BN * CPR / NT;         // chunks per thread per tile (K and V each)
   static_assert(D % 32 == 0, "head dim must be a multiple of 32");
   static_assert(BN % 32 == 0, "tile must hold whole 32-key MFMA blocks");
-  static_assert((BN * CPR) % NT == 0 && NT % CPR == 0, "K tile must split evenly over threads");
-  static_assert(VGR <= NT || VGR % NT == 0, "V tile must split evenly over threads");
+  static_assert((BN * CPR) % NT == 0 && NT % CPR == 0, "tiles must split evenly over threads");
 };
 
 template <class T, int D, int NW, int BN, bool GENERIC>
@@ -64,8 +67,6 @@ void prefill_kernel(const FwdParams p) {
   constexpr int VTILE = Tile::VTILE;
   constexpr int CPR = Tile::CPR;
   constexpr int KPT = Tile::KPT;
-  constexpr int VGR = Tile::VGR;
-  constexpr int VPT = Tile::VPT;
   constexpr int NKC = D / 16;      // 16-dim MFMA k-steps for S^T
   constexpr int NDB = D / 32;      // 32-dim output blocks of O^T
   constexpr int NKB = BN / 32;     // 32-key blocks per tile
@@ -165,31 +166,23 @@ void prefill_kernel(const FwdParams p) {
   }
 
   // ------------------------------------------------------------ tile loads
-  // K: chunk c = tid + i*NT of the tile is row c / CPR, 16-byte column c % CPR.
-  // V: group gi = tid + i*NT holds keys 4*(gi / CPR) + u (u < 4), column gi % CPR.
+  // K and V tiles are copied row-major: chunk c = tid + i*NT of a tile is key
+  // row c / CPR, 16-byte column c % CPR.  Every byte offset goes into the VGPR
+  // offset operand: the range check of a raw buffer load covers that operand
+  // but not the scalar one.
   const uint16_t* kg = static_cast<const uint16_t*>(p.k) + k_base;
   const uint16_t* vg = static_cast<const uint16_t*>(p.v) + v_base;
-  // Every byte offset goes into the VGPR offset operand: the range check of a
-  // raw buffer load covers that operand but not the scalar one.
   const uint32_t k_row_b = (uint32_t)(p.k_ss * 2);
   const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
-  const bool v_owner = VPT * NT == VGR || tid < VGR;   // threads past VGR own no V group
-  uint32_t k_off[KPT], v_off[VPT][4];
+  uint32_t k_off[KPT], v_off[KPT];
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
     const int c = tid + i * NT;
     k_off[i] = (uint32_t)(c / CPR) * k_row_b + (uint32_t)(c % CPR) * 16;
-  }
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int gi = tid % VGR + i * NT;
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      v_off[i][u] = (uint32_t)((gi / CPR) * 4 + u) * v_row_b + (uint32_t)(gi % CPR) * 16;
+    v_off[i] = (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16;
   }
 
-  u32x4 kreg[KPT];
-  u32x4 vreg[VPT][4];
+  u32x4 kreg[KPT], vreg[KPT];
   auto load_tile = [&](int t) {
     const int n0 = t * BN;
     const auto krs = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
@@ -197,37 +190,26 @@ void prefill_kernel(const FwdParams p) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i) kreg[i] = buf_load16(krs, k_off[i], 0);
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        vreg[i][u] = v_owner ? buf_load16(vrs, v_off[i][u], 0) : u32x4{0, 0, 0, 0};
-    }
+    for (int i = 0; i < KPT; ++i) vreg[i] = buf_load16(vrs, v_off[i], 0);
   };
   auto store_tile = [&](int buf) {
     uint16_t* Ks = smem + buf * (KTILE + VTILE);
-    uint16_t* Vt = Ks + KTILE;
+    uint16_t* Vs = Ks + KTILE;
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int c = tid + i * NT;
       store16(Ks + (c / CPR) * KSTR + (c % CPR) * 8, kreg[i]);
-    }
-    if (v_owner) {
-#pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        const int gi = tid % VGR + i * NT;
-        const int ng = gi / CPR, d0 = (gi % CPR) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const int wd = e >> 1;
-          u32x2 pr;
-          pr[0] = __builtin_amdgcn_perm(vreg[i][1][wd], vreg[i][0][wd], sel);
-          pr[1] = __builtin_amdgcn_perm(vreg[i][3][wd], vreg[i][2][wd], sel);
-          *reinterpret_cast<u32x2*>(Vt + (d0 + e) * VSTR + ng * 4) = pr;
-        }
-      }
+      store16(Vs + (c / CPR) * VSTR + (c % CPR) * 8, vreg[i]);
     }
   };
+
+  // V^T operand of O^T += V^T P^T through ds_read_b64_tr_b16.  Within each
+  // 16-lane group the instruction returns to lane i the i-th column of the 4x16
+  // block whose row r is read by lanes 4r..4r+3 (4 elements each).  Lane
+  // (c32, g) needs, for 16-key chunk cc and 32-dim block db, the keys
+  // 16cc + 4g + r and 16cc + 8 + 4g + r (r < 4) at dim db*32 + c32, so lane j
+  // of its group reads key row 16cc + 4g + j/4 (+8), dims 16(c32/16) + 4(j%4).
+  const int vt_lane = (4 * g + (lane & 15) / 4) * VSTR + 16 * (c32 >> 4) + 4 * (lane & 3);
 
   // ------------------------------------------------------------ main loop
   f32x16 acc[NDB];
@@ -259,7 +241,7 @@ void prefill_kernel(const FwdParams p) {
       if (wl >= 0) need_mask = need_mask || n0 < qpos_w_max - wl;
 
       const uint16_t* Ks = smem + buf * (KTILE + VTILE);
-      const uint16_t* Vt = Ks + KTILE;
+      const uint16_t* Vs = Ks + KTILE;
 
       f32x16 s[NKB];
 #pragma unroll
@@ -272,31 +254,44 @@ void prefill_kernel(const FwdParams p) {
         }
       }
 
-      // Scores -> log2 units (GENERIC applies ALiBi and softcap first), mask.
-      float mx = -INFINITY;
+      // GENERIC: scale, ALiBi and softcap, scores -> log2 units.  Otherwise the
+      // scores stay raw (scale > 0) and the scale is folded into the exp2
+      // argument and the max below.
+      if (GENERIC) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-          float x = s[kb][v];
-          if (GENERIC) {
-            x *= p.scale;
+          for (int v = 0; v < 16; ++v) {
+            const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+            float x = s[kb][v] * p.scale;
             if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qp32 - key)), x);
             if (p.softcap > 0.f) {
               // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
               const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
               x = p.softcap - 2.f * p.softcap * __builtin_amdgcn_rcpf(1.f + e2);
             }
-            x *= kLog2e;
+            s[kb][v] = x * kLog2e;
           }
-          if (need_mask && (key < key_lo || key > key_hi)) x = -INFINITY;
-          s[kb][v] = x;
-          mx = fmaxf(mx, x);
         }
       }
-      // Non-generic scores stay raw (scale > 0): the scale is folded into the
-      // exp2 argument below, and into the max here.
+      // Boundary tiles only (a wave-uniform branch): keys outside
+      // [key_lo, key_hi] -> -inf.
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+            if (key < key_lo || key > key_hi) s[kb][v] = -INFINITY;
+          }
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int v = 0; v < 16; v += 2) mx = fmaxf(fmaxf(mx, s[kb][v]), s[kb][v + 1]);
+      }
       const float sl = GENERIC ? 1.f : p.scale_log2;
       mx = halves_max(mx) * sl;
       const bool raise = mx > m_run + kRescaleSlack;
@@ -327,9 +322,9 @@ void prefill_kernel(const FwdParams p) {
         }
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const uint16_t* vrow = Vt + (db * 32 + c32) * VSTR + cc * 16 + g * 4;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+          const uint16_t* vp = Vs + vt_lane + cc * 16 * VSTR + db * 32;
+          const u32x2 lo = lds_read_tr16(vp);
+          const u32x2 hi = lds_read_tr16(vp + 8 * VSTR);
           const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
           acc[db] = T::mfma32(a, pb, acc[db]);
         }
