@@ -9,7 +9,7 @@
 
 #include <string>
 
-#include "../../include/fa_gfx950.h"
+#include "fa_gfx950.h"
 #include "fa_fwd_launch.h"
 
 namespace {

@@ -36,14 +36,19 @@ hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipS
   return hipGetLastError();
 }
 
-// Prefill kernel tiles (fa_prefill_kernel.h) per head dim: 4 waves x 32 rows;
-// 64-key tiles, 32 at D=256 (register budget of the O^T accumulators).
-template <int D> struct PrefillCfg2 { static constexpr int NW = 4, BN = D >= 256 ? 32 : 64; };
-
-template <class T, int D, int NW, int BN, bool GEN>
+// Prefill tile table (fa_prefill_kernel.h), keyed by head dim and by whether
+// the problem is masked (causal, window or varlen):
+//   D = 128, masked  : 4 waves, 32-key tiles, 3 waves per SIMD (165 VGPRs)
+//   D = 128, unmasked: 8 waves (256 query rows share each K/V tile), 64-key tiles
+//   D = 256          : 8 waves, 32-key tiles (the O^T accumulators take 128 VGPRs)
+//   D = 32 / 64      : 4 waves, 64-key tiles
+// Measured on MI355X at B4 H32 S4096 D128: the masked choice is ahead on
+// causal and varlen (less work past the diagonal / sequence end), the
+// unmasked one on non-causal.
+template <class T, int D, int NW, int BN, bool GEN, int WPE>
 hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
   using Tile = PrefillTile<D, NW, BN>;
-  auto kern = prefill_kernel<T, D, NW, BN, GEN>;
+  auto kern = prefill_kernel<T, D, NW, BN, GEN, WPE>;
   static bool lds_attr_set = false;
   if (!lds_attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -60,12 +65,24 @@ hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <class T, int D, bool GEN>
+hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
+  const bool masked = p.causal || p.window_left >= 0 || p.window_right >= 0 || p.cu_q != nullptr;
+  if constexpr (D == 128) {
+    if (masked) return launch_prefill_cfg<T, D, 4, 32, GEN, 3>(p, st);
+    return launch_prefill_cfg<T, D, 8, 64, GEN, 2>(p, st);
+  } else if constexpr (D == 256) {
+    return launch_prefill_cfg<T, D, 8, 32, GEN, 2>(p, st);
+  } else {
+    return launch_prefill_cfg<T, D, 4, 64, GEN, 2>(p, st);
+  }
+}
+
 template <class T, int D, int MODE, bool GEN>
 hipError_t launch_fwd_d(const FwdParams& p, hipStream_t st) {
   if (MODE == kModePrefill) {
     if constexpr (D % 32 == 0) {
-      using C = PrefillCfg2<D>;
-      return launch_prefill_cfg<T, D, C::NW, C::BN, GEN>(p, st);
+      return launch_prefill<T, D, GEN>(p, st);
     } else {
       using C = PrefillCfg<D>;
       return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, p.seqlen_q, p.heads_q * p.batch, st);

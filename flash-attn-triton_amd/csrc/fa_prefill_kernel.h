@@ -49,14 +49,15 @@ struct PrefillTile {
   static constexpr int VTILE = BN * VSTR;
   static constexpr int LDS_BYTES = 2 * (KTILE + VTILE) * 2;
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
-  static constexpr int KPT = BN * CPR / NT;         // chunks per thread per tile (K and V each)
+  static constexpr int CHUNKS = BN * CPR;          // 16-byte chunks per tile (K and V each)
+  static constexpr int KPT = (CHUNKS + NT - 1) / NT; // chunks per thread per tile
   static_assert(D % 32 == 0, "head dim must be a multiple of 32");
   static_assert(BN % 32 == 0, "tile must hold whole 32-key MFMA blocks");
-  static_assert((BN * CPR) % NT == 0 && NT % CPR == 0, "tiles must split evenly over threads");
+  static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
 };
 
-template <class T, int D, int NW, int BN, bool GENERIC>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <class T, int D, int NW, int BN, bool GENERIC, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void prefill_kernel(const FwdParams p) {
   using Tile = PrefillTile<D, NW, BN>;
   constexpr int BM = Tile::BM;
@@ -67,6 +68,7 @@ void prefill_kernel(const FwdParams p) {
   constexpr int VTILE = Tile::VTILE;
   constexpr int CPR = Tile::CPR;
   constexpr int KPT = Tile::KPT;
+  constexpr int CHUNKS = Tile::CHUNKS;
   constexpr int NKC = D / 16;      // 16-dim MFMA k-steps for S^T
   constexpr int NDB = D / 32;      // 32-dim output blocks of O^T
   constexpr int NKB = BN / 32;     // 32-key blocks per tile
@@ -177,29 +179,43 @@ void prefill_kernel(const FwdParams p) {
   uint32_t k_off[KPT], v_off[KPT];
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
+    // Threads past the tile's chunk count load nothing: an offset at the top
+    // of the 32-bit range is beyond any resource and reads zero.
     const int c = tid + i * NT;
-    k_off[i] = (uint32_t)(c / CPR) * k_row_b + (uint32_t)(c % CPR) * 16;
-    v_off[i] = (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16;
+    k_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * k_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
+    v_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
   }
 
   u32x4 kreg[KPT], vreg[KPT];
-  auto load_tile = [&](int t) {
+  auto load_k = [&](int t) {
     const int n0 = t * BN;
-    const auto krs = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
-    const auto vrs = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
+    const auto rs = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) kreg[i] = buf_load16(krs, k_off[i], 0);
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) vreg[i] = buf_load16(vrs, v_off[i], 0);
+    for (int i = 0; i < KPT; ++i) kreg[i] = buf_load16(rs, k_off[i], 0);
   };
-  auto store_tile = [&](int buf) {
-    uint16_t* Ks = smem + buf * (KTILE + VTILE);
-    uint16_t* Vs = Ks + KTILE;
+  auto load_v = [&](int t) {
+    const int n0 = t * BN;
+    const auto rs = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) vreg[i] = buf_load16(rs, v_off[i], 0);
+  };
+  // LDS: [K slot 0][K slot 1][V slot 0][V slot 1].
+  auto k_slot = [&](int i) { return smem + (i & 1) * KTILE; };
+  auto v_slot = [&](int i) { return smem + 2 * KTILE + (i & 1) * VTILE; };
+  auto store_k = [&](int slot) {
+    uint16_t* Ks = k_slot(slot);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int c = tid + i * NT;
-      store16(Ks + (c / CPR) * KSTR + (c % CPR) * 8, kreg[i]);
-      store16(Vs + (c / CPR) * VSTR + (c % CPR) * 8, vreg[i]);
+      if (CHUNKS % NT == 0 || c < CHUNKS) store16(Ks + (c / CPR) * KSTR + (c % CPR) * 8, kreg[i]);
+    }
+  };
+  auto store_v = [&](int slot) {
+    uint16_t* Vs = v_slot(slot);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int c = tid + i * NT;
+      if (CHUNKS % NT == 0 || c < CHUNKS) store16(Vs + (c / CPR) * VSTR + (c % CPR) * 8, vreg[i]);
     }
   };
 
@@ -211,126 +227,165 @@ void prefill_kernel(const FwdParams p) {
   // of its group reads key row 16cc + 4g + j/4 (+8), dims 16(c32/16) + 4(j%4).
   const int vt_lane = (4 * g + (lane & 15) / 4) * VSTR + 16 * (c32 >> 4) + 4 * (lane & 3);
 
-  // ------------------------------------------------------------ main loop
+  // Per-wave tile classification: skipped (no key of the tile visible to any
+  // row of this wave) or masked (some key hidden from some row).
+  auto wave_skips = [&](int t) {
+    const int n0 = t * BN, n1 = n0 + BN;
+    bool skip = !wave_active || n0 >= Sk;
+    if (causal) skip = skip || n0 > qpos_w_max;
+    if (wr >= 0) skip = skip || n0 > qpos_w_max + wr;
+    if (wl >= 0) skip = skip || n1 - 1 < qpos_w_min - wl;
+    return skip;
+  };
+  auto wave_masks = [&](int t) {
+    const int n0 = t * BN, n1 = n0 + BN;
+    bool need = n1 > Sk;
+    if (causal) need = need || n1 - 1 > qpos_w_min;
+    if (wr >= 0) need = need || n1 - 1 > qpos_w_min + wr;
+    if (wl >= 0) need = need || n0 < qpos_w_max - wl;
+    return need;
+  };
+
   f32x16 acc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
   float m_run = -INFINITY;   // running (possibly stale) max, log2 units
   float l_run = 0.f;         // this lane's partial row sum
 
-  if (t_begin < t_end) {
-    load_tile(t_begin);
-    store_tile(0);
-  }
-  for (int t = t_begin; t < t_end; ++t) {
-    const int buf = (t - t_begin) & 1;
-    __syncthreads();
-    const bool has_next = t + 1 < t_end;
-    if (has_next) load_tile(t + 1);
-
-    const int n0 = t * BN;
-    const int n1 = n0 + BN;   // exclusive
-    bool skip = !wave_active || n0 >= Sk;
-    if (causal) skip = skip || n0 > qpos_w_max;
-    if (wr >= 0) skip = skip || n0 > qpos_w_max + wr;
-    if (wl >= 0) skip = skip || n1 - 1 < qpos_w_min - wl;
-    if (!skip) {
-      bool need_mask = n1 > Sk;
-      if (causal) need_mask = need_mask || n1 - 1 > qpos_w_min;
-      if (wr >= 0) need_mask = need_mask || n1 - 1 > qpos_w_min + wr;
-      if (wl >= 0) need_mask = need_mask || n0 < qpos_w_max - wl;
-
-      const uint16_t* Ks = smem + buf * (KTILE + VTILE);
-      const uint16_t* Vs = Ks + KTILE;
-
-      f32x16 s[NKB];
+  // S^T of one tile from a K slot (v_mfma_f32_32x32x16: A = K rows, B = Q^T).
+  auto qk = [&](const uint16_t* Ks, f32x16* sd) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        s[kb] = f32x16{};
+    for (int kb = 0; kb < NKB; ++kb) {
+      sd[kb] = f32x16{};
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
-          const u32x4 a = load16(Ks + (kb * 32 + c32) * KSTR + kc * 16 + g * 8);
-          s[kb] = T::mfma32(a, qreg[kc], s[kb]);
-        }
+      for (int kc = 0; kc < NKC; ++kc) {
+        const u32x4 a = load16(Ks + (kb * 32 + c32) * KSTR + kc * 16 + g * 8);
+        sd[kb] = T::mfma32(a, qreg[kc], sd[kb]);
       }
-
-      // GENERIC: scale, ALiBi and softcap, scores -> log2 units.  Otherwise the
-      // scores stay raw (scale > 0) and the scale is folded into the exp2
-      // argument and the max below.
-      if (GENERIC) {
+    }
+  };
+  // O^T += V^T P^T for one tile from a V slot.
+  auto pv = [&](const uint16_t* Vs, const u32x4* pb) {
 #pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
+    for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-            float x = s[kb][v] * p.scale;
-            if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qp32 - key)), x);
-            if (p.softcap > 0.f) {
-              // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
-              const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
-              x = p.softcap - 2.f * p.softcap * __builtin_amdgcn_rcpf(1.f + e2);
-            }
-            s[kb][v] = x * kLog2e;
-          }
-        }
+      for (int db = 0; db < NDB; ++db) {
+        const uint16_t* vp = Vs + vt_lane + cc * 16 * VSTR + db * 32;
+        const u32x2 lo = lds_read_tr16(vp);
+        const u32x2 hi = lds_read_tr16(vp + 8 * VSTR);
+        const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
+        acc[db] = T::mfma32(a, pb[cc], acc[db]);
       }
-      // Boundary tiles only (a wave-uniform branch): keys outside
-      // [key_lo, key_hi] -> -inf.
-      if (need_mask) {
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-            if (key < key_lo || key > key_hi) s[kb][v] = -INFINITY;
-          }
-        }
-      }
-      float mx = -INFINITY;
+    }
+  };
+  // Softmax of one tile of scores starting at key n0: GENERIC transform,
+  // boundary mask, lazy max / rescale, P = exp2(s - m) packed to the element
+  // type as the B operand of pv (pb[cc] holds keys 16cc .. 16cc + 15 in the
+  // MFMA's k order), row sums.
+  auto softmax_tile = [&](f32x16* sc, int n0, bool masked, u32x4* pb) {
+    // GENERIC: scale, ALiBi and softcap, scores -> log2 units.  Otherwise the
+    // scores stay raw (scale > 0) and the scale is folded into the exp2
+    // argument and the max.
+    if (GENERIC) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-        for (int v = 0; v < 16; v += 2) mx = fmaxf(fmaxf(mx, s[kb][v]), s[kb][v + 1]);
-      }
-      const float sl = GENERIC ? 1.f : p.scale_log2;
-      mx = halves_max(mx) * sl;
-      const bool raise = mx > m_run + kRescaleSlack;
-      if (__builtin_amdgcn_ballot_w64(raise)) {
-        const float m_new = raise ? mx : m_run;
-        const float alpha = m_new == m_run ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
-        m_run = m_new;
-      }
-      const float m_use = m_run == -INFINITY ? 0.f : m_run;
-
-#pragma unroll
-      for (int cc = 0; cc < NCC; ++cc) {
-        f32x16& sv = s[cc >> 1];
-        const int o8 = (cc & 1) * 8;
-        u32x4 pb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
-          const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
-          pb[j] = T::pack2(e0, e1);
-          if (T::kSumRounded)
-            l_run = T::sum2(pb[j], l_run);
-          else
-            l_run += e0 + e1;
-        }
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint16_t* vp = Vs + vt_lane + cc * 16 * VSTR + db * 32;
-          const u32x2 lo = lds_read_tr16(vp);
-          const u32x2 hi = lds_read_tr16(vp + 8 * VSTR);
-          const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-          acc[db] = T::mfma32(a, pb, acc[db]);
+        for (int v = 0; v < 16; ++v) {
+          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+          float x = sc[kb][v] * p.scale;
+          if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qp32 - key)), x);
+          if (p.softcap > 0.f) {
+            // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
+            const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
+            x = p.softcap - 2.f * p.softcap * __builtin_amdgcn_rcpf(1.f + e2);
+          }
+          sc[kb][v] = x * kLog2e;
         }
       }
     }
-    if (has_next) store_tile(buf ^ 1);
+    // Boundary tiles only (a wave-uniform branch): keys outside
+    // [key_lo, key_hi] -> -inf.
+    if (masked) {
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+          if (key < key_lo || key > key_hi) sc[kb][v] = -INFINITY;
+        }
+      }
+    }
+    // Row max over this lane's scores: four independent max3 chains.
+    float mq[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+      for (int v = 0; v < 16; v += 8) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          mq[q] = fmaxf(fmaxf(mq[q], sc[kb][v + 2 * q]), sc[kb][v + 2 * q + 1]);
+      }
+    }
+    const float sl = GENERIC ? 1.f : p.scale_log2;
+    const float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * sl;
+    const bool raise = mx > m_run + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(raise)) {
+      const float m_new = raise ? mx : m_run;
+      const float alpha = m_new == m_run ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float lq[4] = {0.f, 0.f, 0.f, 0.f};   // independent partial row sums
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+      const f32x16& sv = sc[cc >> 1];
+      const int o8 = (cc & 1) * 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
+        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
+        pb[cc][j] = T::pack2(e0, e1);
+        if (T::kSumRounded)
+          lq[j] = T::sum2(pb[cc][j], lq[j]);
+        else
+          lq[j] += e0 + e1;
+      }
+    }
+    l_run += (lq[0] + lq[1]) + (lq[2] + lq[3]);
+  };
+
+  // ------------------------------------------------------------ main loop
+  const int J = t_end - t_begin;
+  // One wave group: per tile S = K Q^T, softmax, O^T += V^T P^T, with the
+  // next tile's loads in flight; LDS slot i & 1 holds K_i and V_i.
+  u32x4 pbuf[NCC];
+  f32x16 s[NKB];
+  if (J > 0) {
+    load_k(t_begin);
+    load_v(t_begin);
+    store_k(0);
+    store_v(0);
+  }
+  for (int it = 0; it < J; ++it) {
+    const int t = t_begin + it;
+    __syncthreads();
+    const bool has_next = it + 1 < J;
+    if (has_next) {
+      load_k(t + 1);
+      load_v(t + 1);
+    }
+    if (!wave_skips(t)) {
+      qk(k_slot(it), s);
+      softmax_tile(s, t * BN, wave_masks(t), pbuf);
+      pv(v_slot(it), pbuf);
+    }
+    if (has_next) {
+      store_k(it + 1);
+      store_v(it + 1);
+    }
   }
 
   // ------------------------------------------------------------ epilogue
