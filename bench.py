@@ -210,6 +210,28 @@ def make_varlen(torch):
                 kernel="fwd_kernel")
 
 
+def make_copy(torch):
+    """Calibration leg for the HBM traffic counters: a device-to-device copy of
+    1 GiB (torch's copy kernel) moves exactly 1 GiB in and 1 GiB out, so
+    FETCH_SIZE / WRITE_SIZE per dispatch of this kernel give the counter's
+    scale factor."""
+    n = 1 << 29
+    src = torch.ones(n, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    nbytes = 2 * src.numel() * 2
+
+    def step():
+        dst.copy_(src)
+        return dst
+
+    cfg = {"workload": "copy_1GiB_fp16", "bytes_read": src.numel() * 2,
+           "bytes_written": src.numel() * 2}
+    return dict(step=step, work=nbytes, unit="GB/s", scale=1e9, dtype="fp16",
+                metric="device copy GB/s (traffic-counter calibration)", bound="hbm",
+                peak=PEAK["hbm"], peak_unit="GB/s", config=cfg, cpu=None,
+                kernel="torch copy kernel")
+
+
 WORKLOADS = {
     "dense_causal": lambda torch: make_dense(torch, True),
     "dense": lambda torch: make_dense(torch, False),
@@ -217,6 +239,7 @@ WORKLOADS = {
     "int8": lambda torch: make_int8(torch, False),
     "decode": make_decode,
     "varlen": make_varlen,
+    "copy": make_copy,
 }
 
 
@@ -261,7 +284,7 @@ def main():
     achieved = wl["work"] / avg_launch_s / wl["scale"]
 
     cpu = None
-    if args.cpu_budget > 0:
+    if args.cpu_budget > 0 and wl["cpu"] is not None:
         torch.set_num_threads(os.cpu_count() or 1)
         cpu = wl["cpu"](args.cpu_budget)
 

@@ -10,6 +10,7 @@
 #include <string>
 
 #include "fa_gfx950.h"
+#include "fa_decode.h"
 #include "fa_fwd_launch.h"
 
 namespace {
@@ -74,31 +75,41 @@ bool needs_generic(const fa::FwdParams& p) {
 }
 
 struct KvPlan {
-  int num_splits, split_tiles;
+  bool decode;                       // decode_kernel (fa_decode.hip) instead of fwd_kernel
+  int num_splits, split_tiles, split_keys;
   int64_t o_part_bytes, lse_part_bytes;
 };
 
 KvPlan kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
-                    int64_t head_dim, int64_t max_keys) {
+                    int64_t head_dim, int64_t max_keys, int64_t page_size) {
   const int64_t group = heads_q / heads_k;
   const int64_t rows = seqlen_q * group;
-  const int tile = fa::kvcache_tile_keys((int)rows, (int)head_dim);
-  const int64_t bm = (rows <= 32 && head_dim <= 128) ? 32 : 128;
-  const int64_t max_tiles = max_keys > 0 ? (max_keys + tile - 1) / tile : 1;
-  const int64_t base = batch * heads_k * ((rows + bm - 1) / bm);
-  // Enough workgroups to cover 256 CUs several times over; at least four key
-  // tiles per split so the merge stays a small fraction of the traffic.
-  const int64_t target = bm == 32 ? 8192 : 1024;
-  int64_t splits = base > 0 ? (target + base - 1) / base : 1;
-  const int64_t cap = max_tiles / 4 > 1 ? max_tiles / 4 : 1;
-  if (splits > cap) splits = cap;
-  if (splits > 256) splits = 256;
+  KvPlan plan{};
+  int64_t splits;
+  if (fa_decode_eligible(rows, head_dim, page_size)) {
+    plan.decode = true;
+    plan.split_keys = fa_decode_split_keys(batch, heads_k, max_keys);
+    splits = max_keys > 0 ? (max_keys + plan.split_keys - 1) / plan.split_keys : 1;
+    plan.split_tiles = 0;
+  } else {
+    const int tile = fa::kvcache_tile_keys((int)rows, (int)head_dim);
+    const int64_t bm = (rows <= 32 && head_dim <= 128) ? 32 : 128;
+    const int64_t max_tiles = max_keys > 0 ? (max_keys + tile - 1) / tile : 1;
+    const int64_t base = batch * heads_k * ((rows + bm - 1) / bm);
+    // Enough workgroups to cover 256 CUs several times over; at least four key
+    // tiles per split so the merge stays a small fraction of the traffic.
+    const int64_t target = bm == 32 ? 8192 : 1024;
+    splits = base > 0 ? (target + base - 1) / base : 1;
+    const int64_t cap = max_tiles / 4 > 1 ? max_tiles / 4 : 1;
+    if (splits > cap) splits = cap;
+    if (splits > 256) splits = 256;
+    if (splits < 1) splits = 1;
+    int64_t split_tiles = (max_tiles + splits - 1) / splits;
+    splits = (max_tiles + split_tiles - 1) / split_tiles;
+    plan.split_tiles = (int)split_tiles;
+  }
   if (splits < 1) splits = 1;
-  int64_t split_tiles = (max_tiles + splits - 1) / splits;
-  splits = (max_tiles + split_tiles - 1) / split_tiles;
-  KvPlan plan;
   plan.num_splits = (int)splits;
-  plan.split_tiles = (int)split_tiles;
   const int64_t prow = splits * batch * seqlen_q * heads_q;
   plan.o_part_bytes = splits > 1 ? ((prow * head_dim * 4 + 255) / 256) * 256 : 0;
   plan.lse_part_bytes = splits > 1 ? prow * 4 : 0;
@@ -233,17 +244,18 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
 }
 
 int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
-                        int64_t head_dim, int64_t max_keys, int32_t* num_splits,
-                        int64_t* workspace_bytes) {
+                        int64_t head_dim, int64_t max_keys, int64_t page_size,
+                        int32_t* num_splits, int64_t* workspace_bytes) {
   if (!num_splits || !workspace_bytes)
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache_plan: null output pointer");
   if (batch < 0 || seqlen_q < 0 || heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0 ||
-      max_keys < 0)
+      max_keys < 0 || page_size < 0)
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache_plan: bad sizes");
   if (!supported_head_dim(head_dim))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache_plan: head_dim %lld not supported",
                 (long long)head_dim);
-  const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys);
+  const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
+                                   page_size);
   *num_splits = plan.num_splits;
   *workspace_bytes = plan.o_part_bytes + plan.lse_part_bytes;
   g_last_error.clear();
@@ -281,7 +293,8 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
       !aligned16(v_cache, v_cache_stride, 3) || !aligned16(out, o_stride, 3))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: tensors must be 16-byte aligned with "
                                     "strides that are multiples of 8 elements");
-  const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys);
+  const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
+                                   block_table ? page_size : 0);
   if (num_splits != plan.num_splits)
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: num_splits %d does not match the plan (%d)",
                 (int)num_splits, plan.num_splits);
@@ -291,6 +304,33 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: workspace too small or misaligned (%lld < %lld)",
                 (long long)workspace_bytes, (long long)(plan.o_part_bytes + plan.lse_part_bytes));
   if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
+  if (plan.decode) {
+    fa::DecodeParams d{};
+    d.q = q; d.k = k_cache; d.v = v_cache; d.o = out; d.lse = lse;
+    d.q_sb = q_stride[0]; d.q_ss = q_stride[1]; d.q_sh = q_stride[2];
+    d.k_sb = k_cache_stride[0]; d.k_ss = k_cache_stride[1]; d.k_sh = k_cache_stride[2];
+    d.v_sb = v_cache_stride[0]; d.v_ss = v_cache_stride[1]; d.v_sh = v_cache_stride[2];
+    d.o_sb = o_stride[0]; d.o_ss = o_stride[1]; d.o_sh = o_stride[2];
+    if (lse) { d.lse_sb = lse_stride[0]; d.lse_sh = lse_stride[1]; d.lse_ss = lse_stride[2]; }
+    d.seqlens = cache_seqlens;
+    d.block_table = block_table; d.bt_stride = block_table_stride; d.page_size = (int)page_size;
+    d.cache_rows = cache_batch_idx; d.leftpad = cache_leftpad;
+    d.batch = (int)batch; d.seqlen_q = (int)seqlen_q; d.heads_q = (int)heads_q;
+    d.heads_k = (int)heads_k; d.group = (int)(heads_q / heads_k); d.max_keys = (int)max_keys;
+    d.scale = softmax_scale; d.scale_log2 = softmax_scale * fa::kLog2e;
+    d.alibi = alibi_slopes; d.alibi_sb = alibi_batch_stride;
+    d.causal = causal != 0;
+    d.window_left = clamp_window(window_left);
+    d.window_right = clamp_window(window_right);
+    d.split_keys = plan.split_keys; d.num_splits = plan.num_splits;
+    if (plan.num_splits > 1) {
+      d.o_part = static_cast<float*>(workspace);
+      d.lse_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.o_part_bytes);
+    }
+    const bool generic = alibi_slopes != nullptr || !(softmax_scale > 0.f);
+    return hip_status(fa_launch_decode(dtype, d, (int)head_dim, generic, (hipStream_t)stream),
+                      "fa_fwd_kvcache decode launch");
+  }
   fa::FwdParams p{};
   p.q = q; p.k = k_cache; p.v = v_cache; p.o = out; p.lse = lse;
   p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];

@@ -135,6 +135,11 @@ hipError_t fa_launch_combine(int dtype, const float* o_part, const float* lse_pa
                              float* lse, int num_splits, int batch, int seqlen_q, int heads,
                              int head_dim, const int64_t* o_stride, const int64_t* lse_stride,
                              hipStream_t st);
+#include "fa_decode.h"
+bool fa_decode_eligible(int64_t rows, int64_t head_dim, int64_t page_size);
+int fa_decode_split_keys(int64_t batch, int64_t heads_k, int64_t max_keys);
+hipError_t fa_launch_decode(int dtype, const fa::DecodeParams& p, int head_dim, bool generic,
+                            hipStream_t st);
 hipError_t fa_launch_quant_k_int8(const void* k, int8_t* k8, float* s_k, int batch, int heads,
                                   int seqlen, int head_dim, const int64_t* k_stride,
                                   hipStream_t st);

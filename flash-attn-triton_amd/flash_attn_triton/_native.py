@@ -46,7 +46,7 @@ _SIGNATURES = {
     "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
                              _i64, _f32, _vp, _i64, _vp]),
-    "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
+    "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
     "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
                               _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp]),
@@ -147,12 +147,12 @@ def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: i
 
 
 def kvcache_plan(batch: int, seqlen_q: int, heads_q: int, heads_k: int, head_dim: int,
-                 max_keys: int):
+                 max_keys: int, page_size: int = 0):
     lib = load()
     splits = ctypes.c_int32(0)
     ws = ctypes.c_int64(0)
     _check(lib.fa_fwd_kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
-                                   ctypes.byref(splits), ctypes.byref(ws)),
+                                   page_size, ctypes.byref(splits), ctypes.byref(ws)),
            "fa_fwd_kvcache_plan")
     return int(splits.value), int(ws.value)
 
@@ -164,10 +164,10 @@ def fwd_kvcache(q, k_cache, v_cache, out, lse, cache_seqlens, block_table, cache
     lib = load()
     B, Sq, Hq, D = q.shape
     Hk = k_cache.shape[2]
-    splits, ws_bytes = kvcache_plan(B, Sq, Hq, Hk, D, max_keys)
+    page_size = k_cache.shape[1] if block_table is not None else 0
+    splits, ws_bytes = kvcache_plan(B, Sq, Hq, Hk, D, max_keys, page_size)
     if ws_bytes > 0 and (workspace is None or workspace.numel() < ws_bytes):
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    page_size = k_cache.shape[1] if block_table is not None else 0
     bt_stride = block_table.stride(0) if block_table is not None else 0
     lse_stride = _strides(lse.stride()) if lse is not None else None
     status = lib.fa_fwd_kvcache(

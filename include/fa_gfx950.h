@@ -87,11 +87,15 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
 /* Split-KV plan for fa_fwd_kvcache: the number of key splits the launch will
  * use and the workspace bytes it needs (0 when num_splits == 1).
  * max_keys bounds every sequence's visible key count (e.g. the cache
- * capacity).  Host-only, no device work.
+ * capacity); page_size is the paged cache's page size, 0 for a batched cache
+ * (it decides whether the bandwidth-bound decode kernel can run: up to 32
+ * query rows per KV head, head_dim 64 or 128, page_size % 32 == 0).
+ * Host-only, no device work.  No counterpart in the reference, whose
+ * KV-cache path loops over the batch in Python.
  */
 int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
-                        int64_t head_dim, int64_t max_keys, int32_t* num_splits,
-                        int64_t* workspace_bytes);
+                        int64_t head_dim, int64_t max_keys, int64_t page_size,
+                        int32_t* num_splits, int64_t* workspace_bytes);
 
 /* Attention of q against a KV cache, paged or batched (decode and chunked
  * prefill against a cache).
