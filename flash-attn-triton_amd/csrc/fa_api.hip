@@ -391,8 +391,11 @@ int fa_fwd_int8(const void* q, const int8_t* k8, const float* s_k, const void* v
   if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_int8: head_dim %lld not in {32,64,128,256}",
                 (long long)head_dim);
-  if (batch < 0 || heads <= 0 || seqlen < 0 || batch * heads > INT32_MAX || seqlen > INT32_MAX / 2)
+  if (batch < 0 || heads <= 0 || seqlen < 0 || batch * heads > INT32_MAX)
     return fail(FA_ERR_INVALID, "fa_fwd_int8: bad sizes");
+  if (seqlen > kMaxLen || seq_len_k < 0 || seq_len_k > kMaxLen || seq_len_q < 0 ||
+      seq_len_q > kMaxLen)
+    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_int8: lengths exceed 2^29");
   if (!aligned16(q, q_stride, 3) || !aligned16(v, v_stride, 3) || !aligned16(out, o_stride, 3) ||
       reinterpret_cast<uintptr_t>(k8) % 16 != 0)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_int8: misaligned tensors");

@@ -11,15 +11,9 @@
 // Floating-point contraction is switched off in these functions: an FMA of
 // (k * r + 0.5) would round once instead of twice and change ties.
 //
-// The attention kernel uses the layout of fwd_kernel (fa_fwd_kernel.h):
-// S^T = K8 Q8^T on v_mfma_i32_32x32x32_i8 (A = K8 tile from LDS, B = Q8^T in
-// VGPRs, quantized once per workgroup), scores scaled in fp32 by
-// s_q * s_k[key] * sm_scale * log2(e), online softmax in fp32, and
-// O^T += V^T P^T on v_mfma_f32_32x32x16_f16 with P rounded to fp16, as the
-// reference keeps PV in FP16 (attention_kernel_int8.py:130-137).  Masked
-// scores are -inf with an empty-row guard (the reference adds -1e6,
-// :113,119, which matches whenever every row sees a key).
-#include "fa_common.h"
+// The attention kernel follows the schedule of prefill_kernel
+// (fa_prefill_kernel.h); see int8_fwd_kernel below.
+#include "fa_prefill_kernel.h"
 
 namespace fa {
 
@@ -97,17 +91,34 @@ template <int D, int NW, int BN>
 struct Int8Tile {
   static constexpr int BM = NW * 32;
   static constexpr int NT = NW * 64;
-  static constexpr int KSTRB = D + 16;   // K8 row pitch in LDS (bytes)
-  static constexpr int VSTR = BN + 4;    // V^T row pitch (halfs)
+  static constexpr int KSTRB = D + 16;   // K8 row pitch in LDS (bytes): 16 B pad
+  static constexpr int VSTR = D + 32;    // V row pitch in LDS (elements), as the fp16 kernel
   static constexpr int KTILE_B = BN * KSTRB;
   static constexpr int SK_B = BN * 4;
-  static constexpr int VTILE_B = D * VSTR * 2;
+  static constexpr int VTILE_B = BN * VSTR * 2;
   static constexpr int BUF_B = KTILE_B + SK_B + VTILE_B;
   static constexpr int LDS_BYTES = 2 * BUF_B;
+  static constexpr int KCH = BN * D / 16;   // 16-byte K8 chunks per tile
+  static constexpr int VCH = BN * D / 8;    // 16-byte V chunks per tile
+  static constexpr int KPT = (KCH + NT - 1) / NT;
+  static constexpr int VPT = (VCH + NT - 1) / NT;
+  static_assert(KCH % NT == 0 || KCH < NT, "K8 tile must split evenly over threads");
+  static_assert(VCH % NT == 0 || VCH < NT, "V tile must split evenly over threads");
 };
 
-template <int D, int NW, int BN>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+// INT8-QK^T attention forward (the role of _attn_fwd_int8,
+// attention_kernel_int8.py:167-217).  Same schedule as prefill_kernel
+// (fa_prefill_kernel.h): a workgroup owns BM = 32 NW query rows, S^T = K8 Q8^T
+// on v_mfma_i32_32x32x32_i8 (A = K8 rows from LDS, B = Q8^T quantized once per
+// row into VGPRs), scores scaled in fp32 by s_q * s_k[key] * sm_scale * log2(e)
+// (the reference's order, :106-107), online softmax with the lazy max, and
+// O^T += V^T P^T on fp16 MFMA with P rounded to fp16 (the reference keeps PV
+// in fp16, :130-137).  K8 / s_k / V tiles are double-buffered in LDS, read
+// with raw buffer loads (rows past seq_len_k read as zero and are masked);
+// masking (-inf, with an empty-row guard; the reference adds -1e6, :113,119)
+// only runs on boundary tiles.
+template <int D, int NW, int BN, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void int8_fwd_kernel(const Int8Params p) {
   using Tile = Int8Tile<D, NW, BN>;
   constexpr int BM = Tile::BM;
@@ -119,18 +130,14 @@ void int8_fwd_kernel(const Int8Params p) {
   constexpr int NKB = BN / 32;
   constexpr int NCC = BN / 16;
   constexpr int KCPR = D / 16;       // 16-byte chunks per K8 row
-  constexpr int KCH = BN * KCPR;
-  constexpr int KPT = (KCH + NT - 1) / NT;
   constexpr int CPR = D / 8;         // 16-byte chunks per V row
-  constexpr int VGR = (BN / 4) * CPR;
-  constexpr int VPT = (VGR + NT - 1) / NT;
-  static_assert(D % 32 == 0 && BN % 32 == 0, "int8 tiles need 32-multiples");
+  constexpr int KCH = Tile::KCH, VCH = Tile::VCH, KPT = Tile::KPT, VPT = Tile::VPT;
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem8[];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c32 = lane & 31;
   const int g = lane >> 5;
 
@@ -141,7 +148,7 @@ void int8_fwd_kernel(const Int8Params p) {
   const int h = bh % p.heads;
   const int b = bh / p.heads;
   const int S = p.seqlen;
-  const int64_t qoff = (int64_t)p.seq_len_k - p.seq_len_q;
+  const int qoff = p.seq_len_k - p.seq_len_q;
   const int Sk = p.seq_len_k < S ? p.seq_len_k : S;
 
   const uint16_t* qg = static_cast<const uint16_t*>(p.q) + (int64_t)b * p.q_sb + (int64_t)h * p.q_sh;
@@ -153,18 +160,20 @@ void int8_fwd_kernel(const Int8Params p) {
   const int row_last = min(row0 + BM, S) - 1;
   const int qi = row0 + w * 32 + c32;
   const bool row_valid = qi < S;
-  const int64_t qpos = qi + qoff;
+  const int qpos = qi + qoff;
   const int wrow0 = row0 + w * 32;
   const bool wave_active = wrow0 <= row_last;
-  const int64_t qpos_w_min = wrow0 + qoff;
-  const int64_t qpos_w_max = min(wrow0 + 31, row_last) + qoff;
+  const int qpos_w_min = wrow0 + qoff;
+  const int qpos_w_max = min(wrow0 + 31, row_last) + qoff;
   const bool causal = p.causal != 0;
+  int key_hi = Sk - 1;
+  if (causal) key_hi = min(key_hi, qpos);
 
-  int64_t k_hi = Sk;
-  if (causal) k_hi = min(k_hi, (int64_t)row_last + qoff + 1);
-  const int t_end = k_hi > 0 ? (int)((k_hi + BN - 1) / BN) : 0;
+  int k_hi = Sk;
+  if (causal) k_hi = min(k_hi, row_last + qoff + 1);
+  const int J = k_hi > 0 ? (k_hi + BN - 1) / BN : 0;
 
-  // ---- quantize this lane's half of its Q row (division form, int8:100)
+  // ---- quantize this lane's half of its Q row (division form, int8:100).
   // Lane (c32, g) holds dims [32kc + 16g, 32kc + 16g + 16) for kc < NKC: the
   // B-operand layout of v_mfma_i32_32x32x32_i8.
   i32x4 q8[NKC];
@@ -199,67 +208,54 @@ void int8_fwd_kernel(const Int8Params p) {
                                     round_half_away(qf[kc][4 * wd + 3] / s_q));
       }
     }
+    __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): retire the Q loads before the loop
   }
   const float row_scale = s_q * p.scale_log2;
 
-  u32x4 kreg[KPT];
-  float skreg = 0.f;
-  u32x4 vreg[VPT][4];
+  // ---- tile loads: raw buffer resources based at the tile's first key row,
+  // ending at key Sk - 1 (rows past it read as zero).  All offsets in VGPRs.
+  const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
+  uint32_t k_off[KPT], v_off[VPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int c = tid + i * NT;
+    k_off[i] = c < KCH ? (uint32_t)(c / KCPR) * D + (uint32_t)(c % KCPR) * 16 : 0xfffffff0u;
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int c = tid + i * NT;
+    v_off[i] = c < VCH ? (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
+  }
+  u32x4 kreg[KPT], vreg[VPT];
+  float skreg = 1.f;
   auto load_tile = [&](int t) {
     const int n0 = t * BN;
+    const int left = Sk - n0;
+    const auto krs = make_rsrc(k8g + (int64_t)n0 * D, left > 0 ? (uint32_t)left * D : 0u);
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int c = tid + i * NT;
-      kreg[i] = u32x4{0, 0, 0, 0};
-      if (c < KCH) {
-        const int n = c / KCPR, cb = (c % KCPR) * 16;
-        if (n0 + n < Sk) kreg[i] = load16(k8g + (int64_t)(n0 + n) * D + cb);
-      }
-    }
+    for (int i = 0; i < KPT; ++i) kreg[i] = buf_load16(krs, k_off[i], 0);
+    const auto vrs = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) vreg[i] = buf_load16(vrs, v_off[i], 0);
     if (tid < BN) skreg = (n0 + tid < Sk) ? skg[n0 + tid] : 1.0f;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      const int gi = tid + i * NT;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) vreg[i][u] = u32x4{0, 0, 0, 0};
-      if (gi < VGR) {
-        const int ng = gi / CPR, d = (gi % CPR) * 8;
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int j = n0 + ng * 4 + u;
-          if (j < Sk) vreg[i][u] = load16(vg + (int64_t)j * p.v_ss + d);
-        }
-      }
-    }
   };
   auto store_tile = [&](int buf) {
     uint8_t* base = smem8 + buf * Tile::BUF_B;
-    uint8_t* Ks = base;
     float* Sks = reinterpret_cast<float*>(base + Tile::KTILE_B);
-    uint16_t* Vt = reinterpret_cast<uint16_t*>(base + Tile::KTILE_B + Tile::SK_B);
+    uint16_t* Vs = reinterpret_cast<uint16_t*>(base + Tile::KTILE_B + Tile::SK_B);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int c = tid + i * NT;
-      if (c < KCH) store16(Ks + (c / KCPR) * KSTRB + (c % KCPR) * 16, kreg[i]);
+      if (KCH % NT == 0 || c < KCH) store16(base + (c / KCPR) * KSTRB + (c % KCPR) * 16, kreg[i]);
     }
-    if (tid < BN) Sks[tid] = skreg;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      const int gi = tid + i * NT;
-      if (gi < VGR) {
-        const int ng = gi / CPR, d0 = (gi % CPR) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-          const int wd = e >> 1;
-          u32x2 pr;
-          pr[0] = __builtin_amdgcn_perm(vreg[i][1][wd], vreg[i][0][wd], sel);
-          pr[1] = __builtin_amdgcn_perm(vreg[i][3][wd], vreg[i][2][wd], sel);
-          *reinterpret_cast<u32x2*>(Vt + (d0 + e) * VSTR + ng * 4) = pr;
-        }
-      }
+      const int c = tid + i * NT;
+      if (VCH % NT == 0 || c < VCH) store16(Vs + (c / CPR) * VSTR + (c % CPR) * 8, vreg[i]);
     }
+    if (tid < BN) Sks[tid] = skreg;
   };
+  const int vt_lane = (4 * g + (lane & 15) / 4) * VSTR + 16 * (c32 >> 4) + 4 * (lane & 3);
 
   f32x16 acc[NDB];
 #pragma unroll
@@ -267,14 +263,14 @@ void int8_fwd_kernel(const Int8Params p) {
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  if (t_end > 0) {
+  if (J > 0) {
     load_tile(0);
     store_tile(0);
   }
-  for (int t = 0; t < t_end; ++t) {
+  for (int t = 0; t < J; ++t) {
     const int buf = t & 1;
     __syncthreads();
-    const bool has_next = t + 1 < t_end;
+    const bool has_next = t + 1 < J;
     if (has_next) load_tile(t + 1);
     const int n0 = t * BN;
     const int n1 = n0 + BN;
@@ -284,9 +280,8 @@ void int8_fwd_kernel(const Int8Params p) {
       bool need_mask = n1 > Sk;
       if (causal) need_mask = need_mask || n1 - 1 > qpos_w_min;
       const uint8_t* base = smem8 + buf * Tile::BUF_B;
-      const uint8_t* Ks = base;
       const float* Sks = reinterpret_cast<const float*>(base + Tile::KTILE_B);
-      const uint16_t* Vt = reinterpret_cast<const uint16_t*>(base + Tile::KTILE_B + Tile::SK_B);
+      const uint16_t* Vs = reinterpret_cast<const uint16_t*>(base + Tile::KTILE_B + Tile::SK_B);
 
       f32x16 s[NKB];
 #pragma unroll
@@ -294,7 +289,7 @@ void int8_fwd_kernel(const Int8Params p) {
         i32x16 si = i32x16{};
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
-          const u32x4 a = load16(Ks + (kb * 32 + c32) * KSTRB + kc * 32 + g * 16);
+          const u32x4 a = load16(base + (kb * 32 + c32) * KSTRB + kc * 32 + g * 16);
           si = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, a), q8[kc], si, 0, 0, 0);
         }
 #pragma unroll
@@ -304,58 +299,61 @@ void int8_fwd_kernel(const Int8Params p) {
           for (int t4 = 0; t4 < 4; ++t4) s[kb][4 * r + t4] = (float)si[4 * r + t4] * sk4[t4];
         }
       }
-
-      float mx = -INFINITY;
+      if (need_mask) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
+        for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float x = s[kb][v];
-          if (need_mask) {
+          for (int v = 0; v < 16; ++v) {
             const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-            bool ok = key < Sk;
-            if (causal) ok = ok && key <= qpos;
-            if (!ok) x = -INFINITY;
+            if (key > key_hi) s[kb][v] = -INFINITY;
           }
-          s[kb][v] = x;
-          mx = fmaxf(mx, x);
         }
       }
-      mx = halves_max(mx);
-      const float m_tile = mx * row_scale;
-      const float m_new = fmaxf(m_run, m_tile);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      float rs = 0.f;
+      float mq[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const float e = exp2f(fmaf(s[kb][v], row_scale, -m_use));
-          s[kb][v] = e;
-          rs += e;
+        for (int v = 0; v < 16; v += 8) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            mq[q] = fmaxf(fmaxf(mq[q], s[kb][v + 2 * q]), s[kb][v + 2 * q + 1]);
         }
       }
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
+      const float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * row_scale;
+      const bool raise = mx > m_run + kRescaleSlack;
+      if (__builtin_amdgcn_ballot_w64(raise)) {
+        const float m_new = raise ? mx : m_run;
+        const float alpha = m_new == m_run ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+        for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+        m_run = m_new;
+      }
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      u32x4 pb[NCC];
+      float lq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int cc = 0; cc < NCC; ++cc) {
         const f32x16& sv = s[cc >> 1];
         const int o8 = (cc & 1) * 8;
-        u32x4 pb;
-        pb[0] = F16::pack2(sv[o8 + 0], sv[o8 + 1]);
-        pb[1] = F16::pack2(sv[o8 + 2], sv[o8 + 3]);
-        pb[2] = F16::pack2(sv[o8 + 4], sv[o8 + 5]);
-        pb[3] = F16::pack2(sv[o8 + 6], sv[o8 + 7]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], row_scale, -m_use));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], row_scale, -m_use));
+          pb[cc][j] = F16::pack2(e0, e1);
+          lq[j] = F16::sum2(pb[cc][j], lq[j]);
+        }
+      }
+      l_run += (lq[0] + lq[1]) + (lq[2] + lq[3]);
+#pragma unroll
+      for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const uint16_t* vrow = Vt + (db * 32 + c32) * VSTR + cc * 16 + g * 4;
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
+          const uint16_t* vp = Vs + vt_lane + cc * 16 * VSTR + db * 32;
+          const u32x2 lo = lds_read_tr16(vp);
+          const u32x2 hi = lds_read_tr16(vp + 8 * VSTR);
           const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
-          acc[db] = F16::mfma32(a, pb, acc[db]);
+          acc[db] = F16::mfma32(a, pb[cc], acc[db]);
         }
       }
     }
@@ -396,11 +394,10 @@ hipError_t launch_quant_k(const void* k, int8_t* k8, float* s_k, int batch, int 
   return hipGetLastError();
 }
 
-template <int D>
-hipError_t launch_int8_fwd(Int8Params p, hipStream_t st) {
-  constexpr int NW = 4, BN = 64;
+template <int D, int NW, int BN, int WPE>
+hipError_t launch_int8_cfg(Int8Params p, hipStream_t st) {
   using Tile = Int8Tile<D, NW, BN>;
-  auto kern = int8_fwd_kernel<D, NW, BN>;
+  auto kern = int8_fwd_kernel<D, NW, BN, WPE>;
   static bool lds_attr_set = false;
   if (!lds_attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -411,9 +408,22 @@ hipError_t launch_int8_fwd(Int8Params p, hipStream_t st) {
   p.n_mblocks = (p.seqlen + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * p.batch * p.heads;
   if (total <= 0) return hipSuccess;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
   p.total_blocks = (int)total;
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
   return hipGetLastError();
+}
+
+// Tile table: causal -> 4 waves, 32-key tiles (less work past the diagonal);
+// otherwise 8 waves sharing 64-key tiles.  D = 256: 8 waves, 32-key tiles.
+template <int D>
+hipError_t launch_int8_fwd(const Int8Params& p, hipStream_t st) {
+  if constexpr (D == 256) {
+    return launch_int8_cfg<D, 8, 32, 2>(p, st);
+  } else {
+    if (p.causal) return launch_int8_cfg<D, 4, 32, D == 128 ? 3 : 2>(p, st);
+    return launch_int8_cfg<D, 8, 64, 2>(p, st);
+  }
 }
 
 }  // namespace fa
