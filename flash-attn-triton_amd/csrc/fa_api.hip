@@ -11,6 +11,7 @@
 
 #include "fa_gfx950.h"
 #include "fa_decode.h"
+#include "fa_probs.h"
 #include "fa_fwd_launch.h"
 
 namespace {
@@ -150,9 +151,12 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
                  const int64_t* k_stride, const int64_t* v_stride, const int64_t* o_stride,
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
-                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream) {
+                 const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
+                 const int64_t* bias_stride, fa_stream_t stream) {
   if (!q || !k || !v || !out || !q_stride || !k_stride || !v_stride || !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_dense: null pointer argument");
+  if (attn_bias && !bias_stride)
+    return fail(FA_ERR_INVALID, "fa_fwd_dense: attn_bias without bias_stride");
   if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_dense: lse without lse_stride");
   if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: dtype %d not supported", dtype);
@@ -187,10 +191,15 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
   p.window_left = clamp_window(window_left);
   p.window_right = clamp_window(window_right);
   p.q_offset = q_pos_offset;
+  if (attn_bias) {
+    p.bias = attn_bias;
+    p.bias_sb = bias_stride[0]; p.bias_sh = bias_stride[1];
+    p.bias_sq = bias_stride[2]; p.bias_sk = bias_stride[3];
+  }
   p.num_splits = 1;
   p.heavy_first = p.causal || p.window_right >= 0;
-  return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim, needs_generic(p),
-                               (hipStream_t)stream),
+  return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim,
+                               needs_generic(p) || attn_bias != nullptr, (hipStream_t)stream),
                     "fa_fwd_dense launch");
 }
 
@@ -362,6 +371,57 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
                           (int)seqlen_q, (int)heads_q, (int)head_dim, o_stride, lse_stride,
                           (hipStream_t)stream);
   return hip_status(e, "fa_fwd_kvcache launch");
+}
+
+int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, float* lse_out,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t heads_q, int64_t heads_k,
+                  int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
+                  const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
+                  const int64_t* bias_stride, fa_stream_t stream) {
+  if (!q || !k || !lse || !probs || !q_stride || !k_stride || !lse_stride)
+    return fail(FA_ERR_INVALID, "fa_attn_probs: null pointer argument");
+  if ((cu_seqlens_q == nullptr) != (cu_seqlens_k == nullptr))
+    return fail(FA_ERR_INVALID, "fa_attn_probs: cu_seqlens_q and cu_seqlens_k go together");
+  if (attn_bias && !bias_stride)
+    return fail(FA_ERR_INVALID, "fa_attn_probs: attn_bias without bias_stride");
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: dtype %d not supported", dtype);
+  if (!supported_head_dim(head_dim))
+    return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: head_dim %lld not supported",
+                (long long)head_dim);
+  if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0 || heads_q <= 0 || heads_k <= 0 ||
+      heads_q % heads_k != 0 || batch * heads_q > 65535)
+    return fail(FA_ERR_INVALID, "fa_attn_probs: bad sizes");
+  if (max_seqlen_q > kMaxLen || max_seqlen_k > kMaxLen || q_pos_offset > kMaxLen ||
+      q_pos_offset < -kMaxLen)
+    return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: lengths or offset exceed 2^29");
+  if (max_seqlen_q > 4 * 65535)
+    return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: max_seqlen_q above 262140 is not supported");
+  if (!aligned16(q, q_stride, 3) || !aligned16(k, k_stride, 3))
+    return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: q/k must be 16-byte aligned with strides "
+                                    "that are multiples of 8 elements");
+  fa::ProbsParams p{};
+  p.q = q; p.k = k; p.lse = lse; p.probs = probs; p.lse_out = lse_out;
+  p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];
+  p.k_sb = k_stride[0]; p.k_ss = k_stride[1]; p.k_sh = k_stride[2];
+  p.lse_sb = lse_stride[0]; p.lse_ss = lse_stride[1]; p.lse_sh = lse_stride[2];
+  p.cu_q = cu_seqlens_q; p.cu_k = cu_seqlens_k;
+  p.batch = (int)batch; p.max_q = (int)max_seqlen_q; p.max_k = (int)max_seqlen_k;
+  p.heads_q = (int)heads_q; p.group = (int)(heads_q / heads_k); p.head_dim = (int)head_dim;
+  p.scale = softmax_scale; p.softcap = softcap;
+  p.alibi = alibi_slopes; p.alibi_sb = alibi_batch_stride;
+  if (attn_bias) {
+    p.bias = attn_bias;
+    p.bias_sb = bias_stride[0]; p.bias_sh = bias_stride[1];
+    p.bias_sq = bias_stride[2]; p.bias_sk = bias_stride[3];
+  }
+  p.causal = causal != 0; p.q_offset = (int)q_pos_offset;
+  p.window_left = clamp_window(window_left);
+  p.window_right = clamp_window(window_right);
+  return hip_status(fa_launch_probs(dtype, p, (hipStream_t)stream), "fa_attn_probs launch");
 }
 
 int fa_quant_k_int8(const void* k, int8_t* k8, float* s_k, int64_t batch, int64_t heads,

@@ -52,6 +52,10 @@ struct FwdParams {
   int batch, seqlen_q, seqlen_k, heads_q, heads_k, group;
   float scale, scale_log2, softcap, softcap_k;   // softcap_k = 2 log2(e) / softcap
   const float* alibi; int64_t alibi_sb;
+  // Optional fp32 additive bias on the scaled scores (after ALiBi, before
+  // softcap), bias[b*bias_sb + h*bias_sh + i*bias_sq + j*bias_sk]; broadcast
+  // dimensions have stride 0.  Dense prefill only.
+  const float* bias; int64_t bias_sb, bias_sh, bias_sq, bias_sk;
   int causal, window_left, window_right;
   int64_t q_offset;
   const int* cu_q; const int* cu_k;
@@ -348,6 +352,9 @@ void fwd_kernel(const FwdParams p) {
           if (GENERIC) {
             x *= p.scale;
             if (p.alibi != nullptr) x -= slope * fabsf((float)(qpos - key));
+            if (MODE == kModePrefill && p.bias != nullptr && row_valid && key < Sk)
+              x += p.bias[(int64_t)b * p.bias_sb + (int64_t)head * p.bias_sh +
+                          (int64_t)qi * p.bias_sq + (int64_t)key * p.bias_sk];
             if (p.softcap > 0.f) x = p.softcap * tanhf(x / p.softcap);
             x *= kLog2e;
           }

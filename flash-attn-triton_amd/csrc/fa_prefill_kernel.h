@@ -127,6 +127,9 @@ void prefill_kernel(const FwdParams p) {
   const int qpos = qi + (int)qoff;
   float slope = 0.f;
   if (GENERIC && p.alibi != nullptr && row_valid) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
+  const float* bias_row = nullptr;
+  if (GENERIC && p.bias != nullptr)
+    bias_row = p.bias + (int64_t)b * p.bias_sb + (int64_t)hh * p.bias_sh + (int64_t)qi * p.bias_sq;
 
   const int wrow0 = row0 + w * 32;
   const bool wave_active = wrow0 <= row_last;
@@ -294,6 +297,7 @@ void prefill_kernel(const FwdParams p) {
           const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
           float x = sc[kb][v] * p.scale;
           if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qp32 - key)), x);
+          if (p.bias != nullptr && row_valid && key < Sk) x += bias_row[(int64_t)key * p.bias_sk];
           if (p.softcap > 0.f) {
             // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
             const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);

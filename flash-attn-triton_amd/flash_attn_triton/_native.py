@@ -42,7 +42,7 @@ _SIGNATURES = {
     "fa_last_error_string": (ctypes.c_char_p, []),
     "fa_fwd_dense": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64,
-                            _i64, _f32, _vp, _i64, _vp]),
+                            _i64, _f32, _vp, _i64, _vp, _i64p, _vp]),
     "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
                              _i64, _f32, _vp, _i64, _vp]),
@@ -50,6 +50,9 @@ _SIGNATURES = {
     "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
                               _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp]),
+    "fa_attn_probs": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                             _i64, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64, _i64,
+                             _f32, _vp, _i64, _vp, _i64p, _vp]),
     "fa_quant_k_int8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _vp]),
     "fa_fwd_int8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p,
                            _i64p, _f32, _int, _i64, _i64, _vp]),
@@ -112,19 +115,54 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offset: int,
-              window_left: int, window_right: int, softcap: float, alibi) -> None:
-    """q [B,Sq,Hq,D], k/v [B,Sk,Hk,D] (BSHD strides), out like q; lse [B,Hq,Sq] or None."""
+              window_left: int, window_right: int, softcap: float, alibi, bias=None) -> None:
+    """q [B,Sq,Hq,D], k/v [B,Sk,Hk,D] (BSHD strides), out like q; lse [B,Hq,Sq] or None;
+    bias None or fp32 [B,Hq,Sq,Sk] (any strides, 0 broadcasts)."""
     lib = load()
     B, Sq, Hq, D = q.shape
     Sk, Hk = k.shape[1], k.shape[2]
     lse_stride = _strides(lse.stride()) if lse is not None else None
+    bias_stride = _strides(bias.stride()) if bias is not None else None
     status = lib.fa_fwd_dense(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), B, Sq, Sk, Hq, Hk, D,
         _strides(q.stride()[:3]), _strides(k.stride()[:3]), _strides(v.stride()[:3]),
         _strides(out.stride()[:3]), lse_stride, dtype_code(q.dtype), float(softmax_scale),
         int(bool(causal)), int(q_pos_offset), int(window_left), int(window_right), float(softcap),
-        _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)), _stream(q.device))
+        _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)), _ptr(bias), bias_stride,
+        _stream(q.device))
     _check(status, "fa_fwd_dense")
+
+
+def attn_probs(q, k, lse, probs, lse_out, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
+               softmax_scale: float, causal: bool, q_pos_offset: int, window_left: int,
+               window_right: int, softcap: float, alibi, bias=None) -> None:
+    """probs fp32 [B,Hq,max_q,max_k] contiguous from q/k and the forward LSE.
+
+    Dense (cu_q None): q [B,Sq,Hq,D], k [B,Sk,Hk,D], lse [B,Hq,Sq].  Varlen: q
+    [Tq,Hq,D], k [Tk,Hk,D], lse [Tq,Hq], cu_* int32 [B+1]; lse_out (or None)
+    gets [B,Hq,max_q] with -inf padding.
+    """
+    lib = load()
+    if cu_q is None:
+        B, Hq, D = q.shape[0], q.shape[2], q.shape[3]
+        Hk = k.shape[2]
+        q_stride, k_stride = q.stride()[:3], k.stride()[:3]
+        ls = lse.stride()
+        lse_stride = (ls[0], ls[2], ls[1])
+    else:
+        B, Hq, D = cu_q.numel() - 1, q.shape[1], q.shape[2]
+        Hk = k.shape[1]
+        q_stride, k_stride = (0,) + tuple(q.stride()[:2]), (0,) + tuple(k.stride()[:2])
+        lse_stride = (0,) + tuple(lse.stride())
+    bias_stride = _strides(bias.stride()) if bias is not None else None
+    status = lib.fa_attn_probs(
+        _ptr(q), _ptr(k), _ptr(lse), _ptr(probs), _ptr(lse_out), _ptr(cu_q), _ptr(cu_k), B,
+        int(max_seqlen_q), int(max_seqlen_k), Hq, Hk, D, _strides(q_stride), _strides(k_stride),
+        _strides(lse_stride), dtype_code(q.dtype), float(softmax_scale), int(bool(causal)),
+        int(q_pos_offset), int(window_left), int(window_right), float(softcap), _ptr(alibi),
+        0 if alibi is None else int(alibi.stride(0)), _ptr(bias), bias_stride,
+        _stream(q.device))
+    _check(status, "fa_attn_probs")
 
 
 def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,

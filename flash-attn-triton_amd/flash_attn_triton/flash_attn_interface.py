@@ -29,6 +29,7 @@ import torch
 
 from .triton_kernel.attention_kernel import (
     DROPOUT_MSG,
+    _kernel_ready,
     _wrap_grad,
     attention,
     attention_varlen,
@@ -63,16 +64,88 @@ def _normalize_alibi(alibi_slopes, batch, heads, device):
     return alibi_slopes.contiguous()
 
 
+def _bias_view(attn_bias, batch, heads, q_len, k_len, device):
+    """``attn_bias`` as an fp32 ``[B, H, Sq, Sk]`` view; broadcast dims get stride 0.
+
+    The reference adds it to the score tensor with torch broadcasting
+    (flash_attn_interface.py:40-41), so any shape that broadcasts to the
+    scores is accepted.
+    """
+    bias = torch.as_tensor(attn_bias, device=device)
+    if bias.device != device:
+        bias = bias.to(device)
+    bias = bias.to(torch.float32)
+    try:
+        return torch.broadcast_to(bias, (batch, heads, q_len, k_len))
+    except RuntimeError as exc:
+        raise ValueError(
+            f"attn_bias of shape {tuple(bias.shape)} does not broadcast to the scores "
+            f"({batch}, {heads}, {q_len}, {k_len})") from exc
+
+
 def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
                           alibi_slopes, attn_bias=None, causal_offset=0):
     """Materialized-probabilities path (``return_attn_probs`` / ``attn_bias``).
 
-    The reference computes this option with dense torch math
-    (flash_attn_interface.py:15-49); it is not built in this HIP-only port yet.
+    Same contract as the reference's dense torch path
+    (flash_attn_interface.py:15-49): scores are scaled, ALiBi is subtracted at
+    ``|i + causal_offset - j|``, ``attn_bias`` is added, softcap applied, the
+    causal/window mask uses ``qpos = i + causal_offset``; returns ``(out [B,Sq,Hq,D],
+    lse [B,Hq,Sq] fp32, probs [B,Hq,Sq,Sk] fp32)`` with -inf LSE and zero
+    probabilities for rows that see no key.  ``out`` and ``lse`` come from the
+    flash kernel (bias applied in its score epilogue), ``probs`` from
+    ``fa_attn_probs``.
     """
-    raise NotImplementedError(
-        "flash_attn_triton (gfx950 HIP build): return_attn_probs=True and attn_bias are not "
-        "implemented by the HIP kernels yet")
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    _check_compute_dtype(q.dtype)
+    batch, q_len, q_heads, head_dim = q.shape
+    k_len = k.shape[1]
+    if head_dim not in (16, 32, 64, 128, 256):
+        raise ValueError("head dimension must be one of 16, 32, 64, 128, or 256")
+    scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
+    bias = None
+    if attn_bias is not None:
+        bias = _bias_view(attn_bias, batch, q_heads, q_len, k_len, q.device)
+    alibi = None
+    if alibi_slopes is not None:
+        alibi = _normalize_alibi(alibi_slopes, batch, q_heads, q.device)
+    out, lse = dense_forward(q, k, v, softmax_scale=scale, causal=causal,
+                             q_pos_offset=causal_offset, window_left=window_size[0],
+                             window_right=window_size[1], softcap=softcap, alibi=alibi,
+                             return_lse=True, bias=bias)
+    probs = torch.empty((batch, q_heads, q_len, k_len), dtype=torch.float32, device=q.device)
+    _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse, probs, None, None, None,
+                       q_len, k_len, scale, causal, causal_offset, window_size[0],
+                       window_size[1], softcap, alibi, bias)
+    return _wrap_grad(out, q, k, v), lse, probs
+
+
+def _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                 max_seqlen_k, dropout_p, softmax_scale, causal, window_size,
+                                 softcap, alibi):
+    """``flash_attn_varlen_func(return_attn_probs=True)`` (reference :642-659).
+
+    Returns ``(out [Tq,Hq,D], lse [B,Hq,max_seqlen_q] fp32 (-inf padding),
+    probs [B,Hq,max_seqlen_q,max_seqlen_k] fp32 (zero padding))``; each
+    sequence is upper-left aligned with local positions.
+    """
+    if dropout_p > 0.0:
+        raise NotImplementedError(DROPOUT_MSG)
+    _check_compute_dtype(q.dtype)
+    batch = cu_seqlens_q.numel() - 1
+    scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else softmax_scale
+    out, lse_tok = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                  max_seqlen_k, softmax_scale=scale, causal=causal,
+                                  window_left=window_size[0], window_right=window_size[1],
+                                  softcap=softcap, alibi=alibi, return_lse=True)
+    lses = torch.empty((batch, q.shape[1], max_seqlen_q), dtype=torch.float32, device=q.device)
+    probs = torch.empty((batch, q.shape[1], max_seqlen_q, max_seqlen_k), dtype=torch.float32,
+                        device=q.device)
+    _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse_tok, probs, lses, cu_seqlens_q,
+                       cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal, 0,
+                       window_size[0], window_size[1], softcap, alibi)
+    return _wrap_grad(out, q, k, v), lses, probs
 
 
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -431,8 +504,9 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     alibi = _normalize_alibi(alibi_slopes, batch_size, q.shape[1], q.device)
     use_alibi = alibi is not None and bool(torch.any(alibi != 0))
     if return_attn_probs:
-        return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
-                                     softcap, alibi)
+        return _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                            max_seqlen_k, dropout_p, softmax_scale, causal,
+                                            window_size, softcap, alibi)
     if dropout_p > 0.0:
         raise NotImplementedError(DROPOUT_MSG)
     _check_compute_dtype(q.dtype)

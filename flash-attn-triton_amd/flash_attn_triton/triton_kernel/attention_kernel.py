@@ -64,11 +64,14 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
 
 def dense_forward(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: int = 0,
                   window_left: int = -1, window_right: int = -1, softcap: float = 0.0,
-                  alibi: Optional[torch.Tensor] = None, return_lse: bool = False):
+                  alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
+                  bias: Optional[torch.Tensor] = None):
     """Run the dense HIP kernel on ``[B, S, H, D]`` tensors (any BSHD strides).
 
-    Returns ``out [B, Sq, Hq, D]`` (contiguous, dtype of q) and, if requested,
-    the natural-log LSE ``[B, Hq, Sq]`` fp32.
+    ``bias`` (optional) is an fp32 ``[B, Hq, Sq, Sk]`` view (broadcast strides
+    allowed) added to the scaled scores.  Returns ``out [B, Sq, Hq, D]``
+    (contiguous, dtype of q) and, if requested, the natural-log LSE
+    ``[B, Hq, Sq]`` fp32.
     """
     qk, kk, vk = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
     B, Sq, Hq, D = q.shape
@@ -77,7 +80,7 @@ def dense_forward(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: 
     if alibi is not None:
         alibi = alibi.to(device=q.device, dtype=torch.float32).contiguous()
     _native.fwd_dense(qk, kk, vk, out, lse, softmax_scale, causal, q_pos_offset, window_left,
-                      window_right, softcap, alibi)
+                      window_right, softcap, alibi, bias)
     return (out, lse) if return_lse else out
 
 

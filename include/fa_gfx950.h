@@ -52,7 +52,11 @@ const char* fa_last_error_string(void);
  * causal keeps kpos <= qpos; window_left/right >= 0 keep
  * qpos-left <= kpos <= qpos+right (negative = unbounded).  alibi_slopes
  * (nullable, fp32) holds slope[b * alibi_batch_stride + h]; softcap > 0 caps
- * scores with softcap*tanh(s/softcap).  lse (nullable, fp32) receives the
+ * scores with softcap*tanh(s/softcap).  attn_bias (nullable, fp32) is added
+ * to the scaled scores after ALiBi and before softcap, as the reference's
+ * materialized path does (flash_attn_interface.py:36-42):
+ * attn_bias[b*bias_stride[0] + h*bias_stride[1] + i*bias_stride[2] +
+ * j*bias_stride[3]] (stride 0 broadcasts).  lse (nullable, fp32) receives the
  * natural-log logsumexp at lse[b*lse_stride[0] + h*lse_stride[1] +
  * i*lse_stride[2]]; rows with no visible key get out = 0 and lse = -inf.
  */
@@ -62,7 +66,8 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
                  const int64_t* k_stride, const int64_t* v_stride, const int64_t* o_stride,
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
-                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream);
+                 const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
+                 const int64_t* bias_stride, fa_stream_t stream);
 
 /* Packed variable-length forward attention.
  *
@@ -129,6 +134,31 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
                    int64_t window_left, int64_t window_right, const float* alibi_slopes,
                    int64_t alibi_batch_stride, int32_t num_splits, void* workspace,
                    int64_t workspace_bytes, fa_stream_t stream);
+
+/* Materialized attention probabilities (return_attn_probs=True).
+ *
+ * Replaces the dense torch math of `_attention_with_probs`
+ * (flash_attn_interface.py:15-49, called at :139-148, :289-298 and, per
+ * sequence, :642-659).  Given the natural-log LSE the forward kernels return,
+ * writes probs[b][h][i][j] = exp(score - lse) as fp32
+ * [batch, heads_q, max_seqlen_q, max_seqlen_k] contiguous, zero for masked
+ * keys, padding and rows whose LSE is -inf.  Dense (cu_seqlens_* NULL): q
+ * [B, Sq, Hq, D] and k [B, Sk, Hk, D] with {batch, seq, head} strides, lse at
+ * {batch, query, head} strides, queries at position i + q_pos_offset.
+ * Varlen: q [Tq, Hq, D], k [Tk, Hk, D] ({unused, token, head} strides), lse
+ * [Tq, Hq] ({unused, token, head}), positions local to each sequence.
+ * lse_out (nullable) receives the LSE as [batch, heads_q, max_seqlen_q] with
+ * -inf padding (the varlen return layout, :644).  Score epilogue and masks as
+ * fa_fwd_dense.
+ */
+int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, float* lse_out,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t heads_q, int64_t heads_k,
+                  int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
+                  const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
+                  const int64_t* bias_stride, fa_stream_t stream);
 
 /* Per-token INT8 quantization of K (fp16), bit-exact with
  * `_quantize_k_rows` (attention_kernel_int8.py:58-79, launched at :232):
