@@ -15,10 +15,16 @@ FLOP convention (reference README.md:226-229): causal 2*B*H*D*S*(S+1),
 non-causal 4*B*H*D*S^2; varlen counts 4*H*D per unmasked (q, k) pair; decode
 is measured in algorithmic bytes (K/V rows read + q + out + block table).
 
-The JSON line carries ``roofline`` (the dominant kernel's algorithmic rate,
-timed with HIP events around each launch on the launch stream, against the
-MI355X published peak) and ``cpu_baseline`` (the float64 numpy oracle timed
-on a bounded sample of the same workload on the host cores).
+The JSON line carries ``roofline`` and ``cpu_baseline``.  ``roofline.achieved``
+is the algorithmic work of one launch divided by the mean duration of the
+C-ABI launch of the dominant kernel (HIP events recorded on the launch stream
+around every such call inside the timed region; for decode the split and
+combine kernels together), against the MI355X published peak.
+``roofline.traffic`` is HBM bytes per launch from two ``rocprofv3 --pmc`` child
+runs (FETCH_SIZE, WRITE_SIZE), each scaled by what the same counter reads for
+a 1 GiB device copy; ``--traffic off`` skips them.  ``cpu_baseline`` is the
+float64 numpy oracle timed on a bounded sample of the same workload with at
+most 16 host threads.
 """
 from __future__ import annotations
 
@@ -32,6 +38,9 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "flash-attn-triton_amd"))
 sys.path.insert(0, ROOT)
+
+# Host threads for the CPU baseline: the box's CPU share for one GPU.
+CPU_THREADS = min(16, os.cpu_count() or 1)
 
 PEAK = {"fp16": 2500.0, "int8_mixed": 1.0 / (0.5 / 5000.0 + 0.5 / 2500.0), "hbm": 8000.0}
 
@@ -54,26 +63,27 @@ def make_dense(torch, causal):
     def cpu(budget_s):
         import numpy as np
         from oracle import attention as ora
-        qc, kc, vc = (t[:1].cpu().numpy() for t in (q, k, v))
-        done, heads, t0 = 0.0, 0, time.perf_counter()
-        while heads < H and (time.perf_counter() - t0) < budget_s:
-            ora.attention(qc[:, :, heads:heads + 1], kc[:, :, heads:heads + 1],
-                          vc[:, :, heads:heads + 1], causal=causal)
+        heads, t0 = 0, time.perf_counter()
+        while heads < B * H and (time.perf_counter() - t0) < budget_s:
+            b, h = divmod(heads, H)
+            qc, kc, vc = (t[b:b + 1, :, h:h + 1].cpu().numpy() for t in (q, k, v))
+            ora.attention(qc, kc, vc, causal=causal)
             heads += 1
         dt = time.perf_counter() - t0
         per_head = flops / (B * H)
         return {"value": per_head * heads / dt / 1e12, "unit": "TFLOP/s",
-                "cores": os.cpu_count(), "kind": "port",
+                "cores": CPU_THREADS, "kind": "port",
                 "sample": f"float64 numpy oracle (oracle/attention.py) on {heads} of {B * H} "
                           f"(batch, head) pairs, S=4096, D=128, causal={causal}; "
-                          f"{dt:.1f} s; OpenBLAS threads = host cores"}
+                          f"{dt:.1f} s; {CPU_THREADS} BLAS threads"}
 
     cfg = {"workload": f"dense_fp16_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
            "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
            "layout": "BSHD contiguous"}
     return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="fp16",
                 metric="attn fwd TFLOP/s (FP16) S=4096 D=128", bound="mfma", peak=PEAK["fp16"],
-                peak_unit="TFLOP/s", config=cfg, cpu=cpu, kernel="fwd_kernel")
+                peak_unit="TFLOP/s", config=cfg, cpu=cpu, native="fwd_dense",
+                kernels=KERNELS["dense"], alg_bytes=4 * B * S * H * D * 2)
 
 
 def make_int8(torch, causal):
@@ -93,15 +103,15 @@ def make_int8(torch, causal):
 
     def cpu(budget_s):
         from oracle import quant
-        qc, kc, vc = (t[:1].cpu().numpy() for t in (q, k, v))
         heads, t0 = 0, time.perf_counter()
-        while heads < H and (time.perf_counter() - t0) < budget_s:
-            quant.attention_int8(qc[:, heads:heads + 1], kc[:, heads:heads + 1],
-                                 vc[:, heads:heads + 1].astype("float64"), causal=causal)
+        while heads < B * H and (time.perf_counter() - t0) < budget_s:
+            b, h = divmod(heads, H)
+            qc, kc, vc = (t[b:b + 1, h:h + 1].cpu().numpy() for t in (q, k, v))
+            quant.attention_int8(qc, kc, vc.astype("float64"), causal=causal)
             heads += 1
         dt = time.perf_counter() - t0
         return {"value": flops / (B * H) * heads / dt / 1e12, "unit": "TFLOP/s",
-                "cores": os.cpu_count(), "kind": "port",
+                "cores": CPU_THREADS, "kind": "port",
                 "sample": f"numpy INT8-QK oracle (oracle/quant.py) on {heads} of {B * H} "
                           f"(batch, head) pairs, S=4096, D=128; {dt:.1f} s"}
 
@@ -111,7 +121,8 @@ def make_int8(torch, causal):
     return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="int8+fp16",
                 metric="attn fwd TFLOP/s (INT8-QK) S=4096 D=128", bound="mfma",
                 peak=PEAK["int8_mixed"], peak_unit="TFLOP/s", config=cfg, cpu=cpu,
-                kernel="int8_fwd_kernel")
+                native="fwd_int8", kernels=KERNELS["int8"],
+                alg_bytes=B * H * S * (3 * D * 2 + D + 4))
 
 
 def make_decode(torch):
@@ -148,7 +159,7 @@ def make_decode(torch):
             done_bytes += int(lengths[b]) * Hk * D * 2 * 2
             b += 1
         dt = time.perf_counter() - t0
-        return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": os.cpu_count(),
+        return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": CPU_THREADS,
                 "kind": "port",
                 "sample": f"float64 numpy oracle (gather through the block table + attention) on "
                           f"{b} of {B} sequences; {dt:.1f} s"}
@@ -158,7 +169,8 @@ def make_decode(torch):
            "cache_lengths": "U[512, 8192], seed 0", "block_table": "random page permutation"}
     return dict(step=step, work=nbytes, unit="GB/s", scale=1e9, dtype="fp16",
                 metric="paged decode GB/s", bound="hbm", peak=PEAK["hbm"], peak_unit="GB/s",
-                config=cfg, cpu=cpu, kernel="fwd_kernel (kvcache split) + combine_kernel")
+                config=cfg, cpu=cpu, native="fwd_kvcache", kernels=KERNELS["decode"],
+                alg_bytes=nbytes)
 
 
 def make_varlen(torch):
@@ -197,7 +209,7 @@ def make_varlen(torch):
             done += 4.0 * H * D * pairs(e - s)
             b += 1
         dt = time.perf_counter() - t0
-        return {"value": done / dt / 1e12, "unit": "TFLOP/s", "cores": os.cpu_count(),
+        return {"value": done / dt / 1e12, "unit": "TFLOP/s", "cores": CPU_THREADS,
                 "kind": "port",
                 "sample": f"float64 numpy oracle on {b} of 32 sequences; {dt:.1f} s"}
 
@@ -207,7 +219,7 @@ def make_varlen(torch):
     return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="fp16",
                 metric="varlen attn fwd TFLOP/s (FP16, causal+window+ALiBi+softcap)",
                 bound="mfma", peak=PEAK["fp16"], peak_unit="TFLOP/s", config=cfg, cpu=cpu,
-                kernel="fwd_kernel")
+                native="fwd_varlen", kernels=KERNELS["varlen"], alg_bytes=4 * T * H * D * 2)
 
 
 def make_copy(torch):
@@ -228,9 +240,21 @@ def make_copy(torch):
            "bytes_written": src.numel() * 2}
     return dict(step=step, work=nbytes, unit="GB/s", scale=1e9, dtype="fp16",
                 metric="device copy GB/s (traffic-counter calibration)", bound="hbm",
-                peak=PEAK["hbm"], peak_unit="GB/s", config=cfg, cpu=None,
-                kernel="torch copy kernel")
+                peak=PEAK["hbm"], peak_unit="GB/s", config=cfg, cpu=None, native=None,
+                kernels=KERNELS["copy"], alg_bytes=nbytes)
 
+
+# The dominant kernel(s) of each workload as rocprofv3 names them; the first
+# one is launched once per step.
+KERNELS = {
+    "dense_causal": ("fa::prefill_kernel",),
+    "dense": ("fa::prefill_kernel",),
+    "int8_causal": ("fa::int8_fwd_kernel",),
+    "int8": ("fa::int8_fwd_kernel",),
+    "decode": ("fa::decode_kernel", "fa::decode_combine_kernel"),
+    "varlen": ("fa::prefill_kernel",),
+    "copy": ("__amd_rocclr_copyBuffer",),
+}
 
 WORKLOADS = {
     "dense_causal": lambda torch: make_dense(torch, True),
@@ -243,6 +267,105 @@ WORKLOADS = {
 }
 
 
+# ----------------------------------------------------------------------------- traffic
+def _counter_per_dispatch(csv_path, counter, kernels):
+    """Mean of ``counter`` (KiB) per launch of ``kernels[0]``, summed over every
+    dispatch of every kernel in ``kernels`` (rocprofv3 counter_collection.csv)."""
+    import csv
+    total, primary = 0.0, 0
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            name = row["Kernel_Name"]
+            hit = [k for k in kernels if k in name]
+            if not hit:
+                continue
+            total += float(row["Counter_Value"])
+            primary += hit[0] == kernels[0]
+    return total / primary if primary else None
+
+
+def _pmc_pass(workload, counter, kernels, outdir):
+    """One ``rocprofv3 --pmc <counter>`` run of this script (a child process,
+    started before this process touches the GPU) -> KiB per dispatch."""
+    import glob
+    import subprocess
+    d = os.path.join(outdir, f"{workload}_{counter}")
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
+           sys.executable, os.path.abspath(__file__), "--workload", workload, "--steps", "2",
+           "--warmup", "1", "--cpu-budget", "0", "--traffic", "off"]
+    subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=180,
+                   check=True)
+    found = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not found:
+        raise RuntimeError(f"rocprofv3 wrote no counter file under {d}")
+    return _counter_per_dispatch(found[0], counter, kernels)
+
+
+def measure_traffic(workload, kernels, keep_dir=None):
+    """HBM bytes per launch of the dominant kernel(s) from FETCH_SIZE and
+    WRITE_SIZE, each scaled by what the same counter reads for a 1 GiB
+    device copy (1 GiB read, 1 GiB written)."""
+    import shutil
+    import tempfile
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not found"
+    copy_kernels = ("__amd_rocclr_copyBuffer",)
+    gib = float(1 << 30)
+    out = {}
+    with tempfile.TemporaryDirectory(prefix="fa_pmc_") as tmp:
+        if keep_dir:
+            os.makedirs(keep_dir, exist_ok=True)
+            tmp = keep_dir
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            cal = _pmc_pass("copy", counter, copy_kernels, tmp)
+            val = _pmc_pass(workload, counter, kernels, tmp)
+            if not cal or val is None:
+                return None, f"{counter}: no matching dispatches"
+            factor = gib / (cal * 1024.0)
+            out[counter] = (val * 1024.0 * factor, factor)
+    return out, None
+
+
+class _LaunchTimer:
+    """Records HIP events on the launch stream around every call of one
+    ``_native`` entry point (the C-ABI launch of the dominant kernel)."""
+
+    def __init__(self, torch, name):
+        self.torch, self.name, self.pairs = torch, name, []
+        self.orig = None
+
+    def __enter__(self):
+        from flash_attn_triton import _native
+        if self.name is None:
+            return self
+        self.orig = getattr(_native, self.name)
+        torch, orig, pairs = self.torch, self.orig, self.pairs
+
+        def timed(*a, **kw):
+            stream = torch.cuda.current_stream()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            r = orig(*a, **kw)
+            e.record(stream)
+            pairs.append((s, e))
+            return r
+
+        setattr(_native, self.name, timed)
+        return self
+
+    def __exit__(self, *exc):
+        if self.orig is not None:
+            from flash_attn_triton import _native
+            setattr(_native, self.name, self.orig)
+        return False
+
+    def mean_s(self):
+        ms = [s.elapsed_time(e) for s, e in self.pairs]
+        return sum(ms) / len(ms) / 1e3 if ms else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -251,12 +374,27 @@ def main():
     ap.add_argument("--workload", default="dense_causal", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=12.0,
                     help="seconds of host work for the CPU baseline sample (0 = skip)")
+    ap.add_argument("--traffic", default="auto", choices=("auto", "off"),
+                    help="auto: two rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE) plus a "
+                         "copy calibration give roofline.traffic; off: traffic null")
+    ap.add_argument("--traffic-dir", default=None,
+                    help="keep the counter runs' rocprofv3 output under this directory")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; every box in this pipeline has one GPU and "
               "the attention forward needs no cross-GPU exchange (see DESIGN.md for how it would "
               "shard). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
+
+    # Counter passes run first, as child processes, while this process has not
+    # touched the GPU yet.
+    traffic, traffic_note = None, None
+    if args.traffic == "auto" and args.workload != "copy":
+        try:
+            traffic, traffic_note = measure_traffic(args.workload, KERNELS[args.workload],
+                                                    args.traffic_dir)
+        except Exception as exc:  # counters are optional: the line is still printed
+            traffic, traffic_note = None, f"counter pass failed: {exc}"
 
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
@@ -266,28 +404,46 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    stream = torch.cuda.current_stream()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step()
-        ends[i].record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    launch_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    avg_launch_s = sum(launch_ms) / len(launch_ms) / 1e3
+    with _LaunchTimer(torch, wl["native"]) as timer:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    avg_launch_s = timer.mean_s()
+    if avg_launch_s is None:   # copy calibration: no native entry point
+        avg_launch_s = wall / args.steps
     ms_per_step = wall / args.steps * 1e3
     value = wl["work"] / (wall / args.steps) / wl["scale"]
     achieved = wl["work"] / avg_launch_s / wl["scale"]
 
     cpu = None
     if args.cpu_budget > 0 and wl["cpu"] is not None:
-        torch.set_num_threads(os.cpu_count() or 1)
-        cpu = wl["cpu"](args.cpu_budget)
+        from threadpoolctl import threadpool_limits
+        torch.set_num_threads(CPU_THREADS)
+        with threadpool_limits(limits=CPU_THREADS):
+            cpu = wl["cpu"](args.cpu_budget)
 
+    roof = {
+        "bound": wl["bound"],
+        "achieved": round(achieved, 3),
+        "peak": round(wl["peak"], 1),
+        "unit": wl["peak_unit"],
+        "frac": round(achieved / wl["peak"], 4),
+        "traffic": None,
+        "kernel": " + ".join(wl["kernels"]),
+        "avg_launch_us": round(avg_launch_s * 1e6, 2),
+    }
+    if traffic is not None:
+        fetch, ffac = traffic["FETCH_SIZE"]
+        write, wfac = traffic["WRITE_SIZE"]
+        roof["traffic"] = round(fetch + write)
+        roof["traffic_detail"] = {"read_bytes": round(fetch), "write_bytes": round(write),
+                                  "fetch_factor": round(ffac, 4), "write_factor": round(wfac, 4),
+                                  "algorithmic_bytes": wl.get("alg_bytes")}
+    elif traffic_note is not None:
+        roof["traffic_note"] = traffic_note
     line = {
         "metric": wl["metric"],
         "value": round(value, 3),
@@ -302,16 +458,7 @@ def main():
         "dtype": wl["dtype"],
         "data": "synthetic (seeded N(0,1))",
         "config": wl["config"],
-        "roofline": {
-            "bound": wl["bound"],
-            "achieved": round(achieved, 3),
-            "peak": round(wl["peak"], 1),
-            "unit": wl["peak_unit"],
-            "frac": round(achieved / wl["peak"], 4),
-            "traffic": None,
-            "kernel": wl["kernel"],
-            "avg_launch_us": round(avg_launch_s * 1e6, 2),
-        },
+        "roofline": roof,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -45,10 +45,10 @@ hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipS
 // Measured on MI355X at B4 H32 S4096 D128: the masked choice is ahead on
 // causal and varlen (less work past the diagonal / sequence end), the
 // unmasked one on non-causal.
-template <class T, int D, int NW, int BN, bool GEN, int WPE>
+template <class T, int D, int NW, int BN, bool GEN, int WPE, bool BIAS = false>
 hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
   using Tile = PrefillTile<D, NW, BN>;
-  auto kern = prefill_kernel<T, D, NW, BN, GEN, WPE>;
+  auto kern = prefill_kernel<T, D, NW, BN, GEN, WPE, BIAS>;
   static bool lds_attr_set = false;
   if (!lds_attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -67,9 +67,22 @@ hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
 
 template <class T, int D, bool GEN>
 hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
+  if constexpr (GEN) {
+    // attn_bias (the materialized-probabilities option): 2 waves per SIMD
+    // leave room for the bias loads.
+    if (p.bias != nullptr) {
+      if constexpr (D == 256) return launch_prefill_cfg<T, D, 8, 32, true, 2, true>(p, st);
+      else return launch_prefill_cfg<T, D, 4, (D == 128 ? 32 : 64), true, 2, true>(p, st);
+    }
+  }
   const bool masked = p.causal || p.window_left >= 0 || p.window_right >= 0 || p.cu_q != nullptr;
   if constexpr (D == 128) {
-    if (masked) return launch_prefill_cfg<T, D, 4, 32, GEN, 3>(p, st);
+    // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
+    // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves.
+    if (masked) {
+      if constexpr (GEN) return launch_prefill_cfg<T, D, 4, 32, GEN, 2>(p, st);
+      else return launch_prefill_cfg<T, D, 4, 32, GEN, 3>(p, st);
+    }
     return launch_prefill_cfg<T, D, 8, 64, GEN, 2>(p, st);
   } else if constexpr (D == 256) {
     return launch_prefill_cfg<T, D, 8, 32, GEN, 2>(p, st);

@@ -56,9 +56,13 @@ struct PrefillTile {
   static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
 };
 
-template <class T, int D, int NW, int BN, bool GENERIC, int WPE>
+// BIAS: the additive fp32 attn_bias is read in the score epilogue (GENERIC
+// only).  It is a separate instantiation because its per-score loads raise
+// register pressure past the budget of the 3-waves-per-SIMD tiles.
+template <class T, int D, int NW, int BN, bool GENERIC, int WPE, bool BIAS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void prefill_kernel(const FwdParams p) {
+  static_assert(GENERIC || !BIAS, "the bias is applied by the generic epilogue");
   using Tile = PrefillTile<D, NW, BN>;
   constexpr int BM = Tile::BM;
   constexpr int NT = Tile::NT;
@@ -128,7 +132,7 @@ void prefill_kernel(const FwdParams p) {
   float slope = 0.f;
   if (GENERIC && p.alibi != nullptr && row_valid) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
   const float* bias_row = nullptr;
-  if (GENERIC && p.bias != nullptr)
+  if (BIAS)
     bias_row = p.bias + (int64_t)b * p.bias_sb + (int64_t)hh * p.bias_sh + (int64_t)qi * p.bias_sq;
 
   const int wrow0 = row0 + w * 32;
@@ -297,7 +301,7 @@ void prefill_kernel(const FwdParams p) {
           const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
           float x = sc[kb][v] * p.scale;
           if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qp32 - key)), x);
-          if (p.bias != nullptr && row_valid && key < Sk) x += bias_row[(int64_t)key * p.bias_sk];
+          if (BIAS && row_valid && key < Sk) x += bias_row[(int64_t)key * p.bias_sk];
           if (p.softcap > 0.f) {
             // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
             const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);

@@ -37,6 +37,7 @@ from .triton_kernel.attention_kernel import (
     varlen_forward,
 )
 from . import _native
+from ._checks import Deferred
 
 BLOCK_SIZE = 64
 
@@ -344,6 +345,7 @@ def flash_attn_with_kvcache(
     Returns (batch, seqlen_q, nheads, headdim).
     """
     paged = block_table is not None
+    chk = Deferred()
     if (rotary_cos is None) != (rotary_sin is None):
         raise ValueError("rotary_cos and rotary_sin must be supplied together")
     if q.ndim != 4 or k_cache.ndim != 4 or v_cache.ndim != 4:
@@ -355,60 +357,75 @@ def flash_attn_with_kvcache(
             raise ValueError("block_table must have shape (batch, max_num_pages)")
         if block_table.dtype not in (torch.int32, torch.int64):
             raise ValueError("block_table must contain integer page indices")
-        if torch.any(block_table < 0) or torch.any(block_table >= k_cache.shape[0]):
-            raise ValueError("block_table contains an invalid physical page index")
+        if block_table.numel():
+            chk.check((block_table < 0).any() | (block_table >= k_cache.shape[0]).any(),
+                      ValueError("block_table contains an invalid physical page index"))
         if cache_leftpad is not None:
-            raise ValueError("cache_leftpad cannot be combined with paged KV caches")
+            chk.fail(ValueError("cache_leftpad cannot be combined with paged KV caches"))
         page_size = k_cache.shape[1]
         cache_capacity = block_table.shape[1] * page_size
     else:
         cache_capacity = k_cache.shape[1]
     if q.shape[-1] != k_cache.shape[-1]:
-        raise ValueError("q and KV cache dimensions are incompatible")
+        chk.fail(ValueError("q and KV cache dimensions are incompatible"))
     if q.device != k_cache.device or q.device != v_cache.device:
-        raise ValueError("q and KV caches must be on the same device")
+        chk.fail(ValueError("q and KV caches must be on the same device"))
     if q.dtype != k_cache.dtype or q.dtype != v_cache.dtype:
-        raise ValueError("q and KV caches must have the same dtype")
+        chk.fail(ValueError("q and KV caches must have the same dtype"))
     if paged and cache_batch_idx is not None:
-        raise ValueError("cache_batch_idx cannot be combined with paged KV caches")
+        chk.fail(ValueError("cache_batch_idx cannot be combined with paged KV caches"))
     if cache_batch_idx is None:
         cache_rows = None
     else:
         cache_rows = torch.as_tensor(cache_batch_idx, device=q.device, dtype=torch.long).flatten()
-        if (cache_rows.numel() != q.shape[0] or torch.any(cache_rows < 0)
-                or torch.any(cache_rows >= k_cache.shape[0])):
-            raise ValueError("cache_batch_idx must contain valid cache-row indices")
+        bad_rows = ValueError("cache_batch_idx must contain valid cache-row indices")
+        if cache_rows.numel() != q.shape[0]:
+            chk.fail(bad_rows)
+        if cache_rows.numel():
+            chk.check((cache_rows < 0).any() | (cache_rows >= k_cache.shape[0]).any(), bad_rows)
     if cache_leftpad is None:
         leftpads = None
     else:
         leftpads = torch.as_tensor(cache_leftpad, device=q.device, dtype=torch.long).flatten()
-        if leftpads.numel() != q.shape[0] or torch.any(leftpads < 0):
-            raise ValueError("cache_leftpad must contain one non-negative value per query batch")
+        bad_pads = ValueError("cache_leftpad must contain one non-negative value per query batch")
+        if leftpads.numel() != q.shape[0]:
+            chk.fail(bad_pads)
+        if leftpads.numel():
+            chk.check((leftpads < 0).any(), bad_pads)
     zero_pad = 0 if leftpads is None else leftpads
     if k is not None or v is not None:
-        raise NotImplementedError(
+        chk.fail(NotImplementedError(
             "flash_attn_triton (gfx950 HIP build): appending k/v to the cache is not "
-            "implemented yet")
+            "implemented yet"))
     if rotary_cos is not None:
-        raise NotImplementedError(
+        chk.fail(NotImplementedError(
             "flash_attn_triton (gfx950 HIP build): rotary embedding in "
-            "flash_attn_with_kvcache is not implemented yet")
+            "flash_attn_with_kvcache is not implemented yet"))
     if cache_seqlens is None:
         lengths = torch.full((q.shape[0],), cache_capacity, dtype=torch.int64, device=q.device)
     else:
         lengths = torch.as_tensor(cache_seqlens, device=q.device, dtype=torch.int64).flatten()
-    if (lengths.numel() != q.shape[0] or torch.any(lengths < 0)
-            or torch.any(lengths + zero_pad > cache_capacity)):
-        raise ValueError("cache_seqlens must contain valid lengths for every batch item")
+    bad_lengths = ValueError("cache_seqlens must contain valid lengths for every batch item")
+    if lengths.numel() != q.shape[0]:
+        chk.fail(bad_lengths)
+    if lengths.numel():
+        chk.check((lengths < 0).any() | (lengths + zero_pad > cache_capacity).any(), bad_lengths)
     if q.shape[-1] not in (16, 32, 64, 128, 256):
-        raise ValueError("head dimension must be one of 16, 32, 64, 128, or 256")
+        chk.fail(ValueError("head dimension must be one of 16, 32, 64, 128, or 256"))
     if q.shape[2] % k_cache.shape[2] != 0:
-        raise ValueError("The number of query heads must be divisible by KV heads")
-    _check_compute_dtype(q.dtype)
+        chk.fail(ValueError("The number of query heads must be divisible by KV heads"))
+    if q.dtype == torch.float32:
+        chk.fail(NotImplementedError(_FP32_MSG))
     if q.shape[0] == 0:
+        chk.flush()
         return q.new_empty(q.shape)
-    alibi = _normalize_alibi(alibi_slopes, q.shape[0], q.shape[2], q.device)
-    if alibi is not None and not bool(torch.any(alibi != 0)):
+    try:
+        alibi = _normalize_alibi(alibi_slopes, q.shape[0], q.shape[2], q.device)
+    except ValueError as exc:
+        chk.fail(exc)
+    alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
+    values = chk.flush()   # the one host synchronization of this call
+    if alibi is not None and not values[alibi_any]:
         alibi = None
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
@@ -418,7 +435,7 @@ def flash_attn_with_kvcache(
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     _native.fwd_kvcache(
         qk, kc, vc, out, None, lengths.to(torch.int32).contiguous(),
-        block_table.to(torch.int32).contiguous() if paged else None,
+        block_table.to(device=q.device, dtype=torch.int32).contiguous() if paged else None,
         cache_rows.to(torch.int32).contiguous() if cache_rows is not None else None,
         leftpads.to(torch.int32).contiguous() if leftpads is not None else None,
         int(cache_capacity), softmax_scale, causal, window_size[0], window_size[1], alibi)
@@ -461,55 +478,71 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         raise ValueError("cu_seqlens arrays must be one-dimensional")
     if cu_seqlens_q.numel() != cu_seqlens_k.numel():
         raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same batch size")
-    if cu_seqlens_q.numel() == 0 or cu_seqlens_q[0].item() != 0 or cu_seqlens_k[0].item() != 0:
-        raise ValueError("cu_seqlens arrays must start at zero and contain a batch boundary")
-    if (torch.any(cu_seqlens_q[1:] < cu_seqlens_q[:-1]) or
-            torch.any(cu_seqlens_k[1:] < cu_seqlens_k[:-1])):
-        raise ValueError("cu_seqlens arrays must be monotonically non-decreasing")
-    if cu_seqlens_q[-1].item() > q.shape[0] or cu_seqlens_k[-1].item() > k.shape[0]:
-        raise ValueError("cu_seqlens values exceed the packed tensor sizes")
+    chk = Deferred()
+    bad_start = ValueError("cu_seqlens arrays must start at zero and contain a batch boundary")
+    if cu_seqlens_q.numel() == 0:
+        raise bad_start
+    chk.check(cu_seqlens_q[0] != 0, bad_start)
+    chk.check(cu_seqlens_k[0] != 0, bad_start)
+    if cu_seqlens_q.numel() > 1:
+        bad_order = ValueError("cu_seqlens arrays must be monotonically non-decreasing")
+        chk.check((cu_seqlens_q[1:] < cu_seqlens_q[:-1]).any(), bad_order)
+        chk.check((cu_seqlens_k[1:] < cu_seqlens_k[:-1]).any(), bad_order)
+    bad_size = ValueError("cu_seqlens values exceed the packed tensor sizes")
+    chk.check(cu_seqlens_q[-1] > q.shape[0], bad_size)
+    chk.check(cu_seqlens_k[-1] > k.shape[0], bad_size)
     if (q.dtype not in (torch.float16, torch.bfloat16, torch.float32) or k.dtype != q.dtype
             or v.dtype != q.dtype):
-        raise ValueError("flash_attn_varlen_func supports matching FP16, BF16 or FP32 tensors")
+        chk.fail(ValueError(
+            "flash_attn_varlen_func supports matching FP16, BF16 or FP32 tensors"))
     if not (q.is_cuda and k.is_cuda and v.is_cuda):
-        raise ValueError("All attention tensors must be CUDA tensors")
+        chk.fail(ValueError("All attention tensors must be CUDA tensors"))
     if q.device != k.device or q.device != v.device:
-        raise ValueError("q, k, and v must be on the same CUDA device")
+        chk.fail(ValueError("q, k, and v must be on the same CUDA device"))
     if q.shape[-1] != k.shape[-1] or k.shape[-1] != v.shape[-1]:
-        raise ValueError("q, k, and v must have the same head dimension")
+        chk.fail(ValueError("q, k, and v must have the same head dimension"))
     if q.shape[-1] not in (16, 32, 64, 128, 256):
-        raise ValueError("head dimension must be one of 16, 32, 64, 128, or 256")
+        chk.fail(ValueError("head dimension must be one of 16, 32, 64, 128, or 256"))
     if q.shape[1] % k.shape[1] != 0:
-        raise ValueError("The number of query heads must be divisible by KV heads")
+        chk.fail(ValueError("The number of query heads must be divisible by KV heads"))
     if dropout_p < 0.0 or dropout_p >= 1.0:
-        raise ValueError("dropout_p must be in the range [0, 1)")
+        chk.fail(ValueError("dropout_p must be in the range [0, 1)"))
     if softcap < 0.0:
-        raise ValueError("softcap must be non-negative")
+        chk.fail(ValueError("softcap must be non-negative"))
     if cu_seqlens_q.device != q.device or cu_seqlens_k.device != q.device:
-        raise ValueError("cu_seqlens arrays must be on the same CUDA device as q, k, and v")
+        chk.fail(ValueError(
+            "cu_seqlens arrays must be on the same CUDA device as q, k, and v"))
     cu_seqlens_q = cu_seqlens_q.to(dtype=torch.int32).contiguous()
     cu_seqlens_k = cu_seqlens_k.to(dtype=torch.int32).contiguous()
     if max_seqlen_q < 0 or max_seqlen_k < 0:
-        raise ValueError("max sequence lengths must be non-negative")
-    if cu_seqlens_q[-1].item() != q.shape[0] or cu_seqlens_k[-1].item() != k.shape[0]:
-        raise ValueError("cu_seqlens arrays must cover the packed q and KV tensors")
+        chk.fail(ValueError("max sequence lengths must be non-negative"))
+    bad_cover = ValueError("cu_seqlens arrays must cover the packed q and KV tensors")
+    chk.check(cu_seqlens_q[-1] != q.shape[0], bad_cover)
+    chk.check(cu_seqlens_k[-1] != k.shape[0], bad_cover)
     if cu_seqlens_q.numel() < 2:
-        raise ValueError("cu_seqlens arrays must describe at least one sequence")
-    actual_max_q = int((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max().item())
-    actual_max_k = int((cu_seqlens_k[1:] - cu_seqlens_k[:-1]).max().item())
-    if max_seqlen_q < actual_max_q or max_seqlen_k < actual_max_k:
-        raise ValueError("max sequence lengths must cover every packed sequence")
+        chk.fail(ValueError("cu_seqlens arrays must describe at least one sequence"))
+    chk.check(((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max() > max_seqlen_q) |
+              ((cu_seqlens_k[1:] - cu_seqlens_k[:-1]).max() > max_seqlen_k),
+              ValueError("max sequence lengths must cover every packed sequence"))
     if max_seqlen_q == 0 or max_seqlen_k == 0:
+        chk.flush()
         return q.new_zeros((q.shape[0], q.shape[1], q.shape[2]))
-    alibi = _normalize_alibi(alibi_slopes, batch_size, q.shape[1], q.device)
-    use_alibi = alibi is not None and bool(torch.any(alibi != 0))
+    try:
+        alibi = _normalize_alibi(alibi_slopes, batch_size, q.shape[1], q.device)
+    except ValueError as exc:
+        chk.fail(exc)
+    alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
     if return_attn_probs:
+        chk.flush()
         return _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                             max_seqlen_k, dropout_p, softmax_scale, causal,
                                             window_size, softcap, alibi)
     if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
-    _check_compute_dtype(q.dtype)
+        chk.fail(NotImplementedError(DROPOUT_MSG))
+    if q.dtype == torch.float32:
+        chk.fail(NotImplementedError(_FP32_MSG))
+    values = chk.flush()   # the one host synchronization of this call
+    use_alibi = alibi is not None and bool(values[alibi_any])
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,

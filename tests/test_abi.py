@@ -125,3 +125,42 @@ def test_python_api_validation_on_cpu():
     with pytest.raises(ValueError):
         flash_attn_varlen_func(q[0], q[0], q[0], cu, torch.tensor([0, 2, 4], dtype=torch.int32),
                                4, 4)
+
+
+def test_deferred_checks_keep_the_reference_order():
+    """Device-side checks are read with one synchronization, but a later host
+    check never overtakes an earlier failing device check."""
+    from flash_attn_triton._checks import Deferred
+    chk = Deferred()
+    chk.check(torch.tensor(False), ValueError("first"))
+    chk.check(torch.tensor(True), ValueError("second"))
+    with pytest.raises(ValueError, match="second"):
+        chk.fail(RuntimeError("host"))
+    chk = Deferred()
+    chk.check(torch.tensor(False), ValueError("first"))
+    with pytest.raises(RuntimeError, match="host"):
+        chk.fail(RuntimeError("host"))
+    chk = Deferred()
+    i = chk.value(torch.tensor(7))
+    chk.check(torch.tensor(False), ValueError("never"))
+    assert chk.flush()[i] == 7
+    assert chk.flush() == []
+
+
+def test_varlen_cu_seqlens_errors_before_device_errors():
+    """Reference order (flash_attn_interface.py:583-598): cu_seqlens checks run
+    before the CUDA-tensor check."""
+    from flash_attn_triton import flash_attn_varlen_func
+    q = torch.zeros(4, 2, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="start at zero"):
+        flash_attn_varlen_func(q, q, q, torch.tensor([1, 4], dtype=torch.int32),
+                               torch.tensor([0, 4], dtype=torch.int32), 4, 4)
+    with pytest.raises(ValueError, match="monotonically"):
+        flash_attn_varlen_func(q, q, q, torch.tensor([0, 3, 2, 4], dtype=torch.int32),
+                               torch.tensor([0, 1, 2, 4], dtype=torch.int32), 4, 4)
+    with pytest.raises(ValueError, match="exceed"):
+        flash_attn_varlen_func(q, q, q, torch.tensor([0, 5], dtype=torch.int32),
+                               torch.tensor([0, 4], dtype=torch.int32), 4, 4)
+    with pytest.raises(ValueError, match="CUDA tensors"):
+        flash_attn_varlen_func(q, q, q, torch.tensor([0, 4], dtype=torch.int32),
+                               torch.tensor([0, 4], dtype=torch.int32), 4, 4)
