@@ -4,6 +4,7 @@
 #pragma once
 
 #include "fa_prefill_kernel.h"
+#include "fa_prefill_pp.h"
 
 namespace fa {
 
@@ -65,6 +66,27 @@ hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Ping-pong prefill (fa_prefill_pp.h): 8 waves, 256 query rows per workgroup.
+template <class T, int D, bool GEN>
+hipError_t launch_prefill_pp(FwdParams p, hipStream_t st) {
+  using Tile = PingPongTile<D>;
+  auto kern = prefill_pp_kernel<T, D, GEN>;
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    lds_attr_set = true;
+  }
+  p.n_mblocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
+  const int64_t total = (int64_t)p.n_mblocks * p.heads_q * p.batch;
+  if (total <= 0) return hipSuccess;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+  p.total_blocks = (int)total;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  return hipGetLastError();
+}
+
 template <class T, int D, bool GEN>
 hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
   if constexpr (GEN) {
@@ -77,6 +99,7 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
   }
   const bool masked = p.causal || p.window_left >= 0 || p.window_right >= 0 || p.cu_q != nullptr;
   if constexpr (D == 128) {
+    if constexpr (!GEN) return launch_prefill_pp<T, D, GEN>(p, st);
     // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
     // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves.
     if (masked) {

@@ -66,6 +66,39 @@ def test_ragged_and_rectangular(sq, sk, causal):
     _check(q, k, v, causal=causal)
 
 
+@pytest.mark.parametrize("sq,sk", [(1, 1), (7, 300), (64, 64), (255, 255), (256, 256), (257, 64),
+                                   (300, 1000), (513, 130), (1000, 257)])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_d128_tile_edges(sq, sk, causal, dtype):
+    # Head dim 128 runs the 256-row / 64-key two-group kernel: lengths on and
+    # around its workgroup (256) and key-tile (64) boundaries, rectangular
+    # both ways, with GQA.
+    q = randn((2, sq, 4, 128), 14, dtype)
+    k = randn((2, sk, 2, 128), 15, dtype)
+    v = randn((2, sk, 2, 128), 16, dtype)
+    _check(q, k, v, dtype, causal=causal)
+
+
+@pytest.mark.parametrize("offset", [-70, 5, 300])
+def test_d128_query_offset(offset):
+    # Cross attention with shifted query positions (causal alignment offset).
+    q = randn((1, 333, 2, 128), 17)
+    k = randn((1, 400, 2, 128), 18)
+    v = randn((1, 400, 2, 128), 19)
+    _check(q, k, v, causal=True, q_pos_offset=offset)
+
+
+def test_d128_strided_packed():
+    q, k, v = (randn((2, 300, 2, 128), s) for s in (94, 95, 96))
+    packed = torch.stack((q, k, v), dim=2).to(DEV)
+    qs, ks, vs = packed.unbind(dim=2)
+    from flash_attn_triton.triton_kernel.attention_kernel import dense_forward
+    out = dense_forward(qs, ks, vs, softmax_scale=0.1, causal=False).cpu()
+    ref, _ = _oracle(q, k, v, softmax_scale=0.1, causal=False)
+    assert_close(to_np(out), ref, ATOL[torch.float16], "packed d128", torch.float16)
+
+
 @pytest.mark.parametrize("hq,hk", [(8, 2), (8, 1), (6, 3)])
 @pytest.mark.parametrize("causal", [False, True])
 def test_gqa(hq, hk, causal):
