@@ -15,9 +15,9 @@
 //    no barrier inside the loop.
 //  * Query rows r = i * G + (h % G) (query i, the G query heads of the KV
 //    head) form the B operand Q^T of S^T = K Q^T on v_mfma_f32_32x32x16, so up
-//    to 32 rows share every K/V byte.  K tiles go straight from memory into
-//    the A-operand registers (each lane one key row, 16 bytes per MFMA step);
-//    V tiles pass through a per-wave LDS slot and come back as the V^T
+//    to 32 rows share every K/V byte.  K and V tiles are loaded row-coalesced
+//    into registers and pass through per-wave LDS slots: K comes back in the
+//    A-operand layout (ds_read_b128 from a swizzled slot), V as the V^T
 //    operand of O^T += V^T P^T through ds_read_b64_tr_b16.
 //  * Two K register sets alternate and V's next load starts as soon as the
 //    current V tile is in LDS, so every wave keeps about two tiles of loads in
@@ -44,9 +44,10 @@ template <int D>
 struct DecodeTile {
   static constexpr int VSTR = D + 32;                       // V row pitch in LDS (elements)
   static constexpr int VSLOT = kDecodeBN * VSTR;            // one wave's V tile (elements)
-  static constexpr int V_BYTES = kDecodeWaves * VSLOT * 2;
+  static constexpr int KSLOT = kDecodeBN * D;               // one wave's K tile (elements, swizzled)
+  static constexpr int KV_BYTES = kDecodeWaves * (VSLOT + KSLOT) * 2;
   static constexpr int MERGE_BYTES = kDecodeWaves * 32 * (D + 2) * 4;   // O rows + (m, l)
-  static constexpr int LDS_BYTES = V_BYTES > MERGE_BYTES ? V_BYTES : MERGE_BYTES;
+  static constexpr int LDS_BYTES = KV_BYTES > MERGE_BYTES ? KV_BYTES : MERGE_BYTES;
 };
 
 template <class T, int D, bool GENERIC>
@@ -72,12 +73,15 @@ void decode_kernel(const DecodeParams p) {
 
   // KV heads vary fastest across workgroups: the heads of one (sequence,
   // split) run together and read the same token rows of the cache (each row
-  // holds all heads), which keeps DRAM pages open.
+  // holds all heads), which keeps DRAM pages open.  The split index varies
+  // slowest: every sequence's full leading splits are dispatched first and
+  // the short or empty trailing ones last, which trims the tail of the grid
+  // (measured 5 % at config 4).
   int id = blockIdx.x;
   const int kvh = id % p.heads_k;
   id /= p.heads_k;
-  const int split = id % p.num_splits;
-  const int b = id / p.num_splits;
+  const int b = id % p.batch;
+  const int split = id / p.batch;
 
   const int L = p.seqlens != nullptr ? p.seqlens[b] : p.max_keys;
   const int k_begin = split * p.split_keys;
@@ -140,7 +144,13 @@ void decode_kernel(const DecodeParams p) {
   const uint16_t* kg = static_cast<const uint16_t*>(p.k);
   const uint16_t* vg = static_cast<const uint16_t*>(p.v);
   uint16_t* vslot = smem + w * Tile::VSLOT;
+  uint16_t* kslot = smem + kDecodeWaves * Tile::VSLOT + w * Tile::KSLOT;
   const int vt_lane = (4 * g + (lane & 15) / 4) * VSTR + 16 * (c32 >> 4) + 4 * (lane & 3);
+  // K tile in LDS: rows of D halfs without padding, 16-byte chunk c of row r
+  // at chunk position c ^ (r % 16) (D = 128) or c ^ (r % 8) (D = 64), so the
+  // 16 rows one quarter-wave reads for an MFMA step land on distinct banks.
+  constexpr int KSW = CPR >= 16 ? 15 : CPR - 1;
+  auto k_lds_ofs = [&](int row, int chunk) { return row * D + ((chunk ^ (row & KSW)) << 3); };
 
   const int n_tiles = (k_end - k_begin + BN - 1) / BN;
   // Loads of tile tt through raw buffer resources based at the tile's first
@@ -149,7 +159,12 @@ void decode_kernel(const DecodeParams p) {
   // (a tile spans 32 rows of at most a page).
   const uint32_t k_row_b = (uint32_t)(p.k_ss * 2);
   const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
-  const uint32_t k_voff = (uint32_t)c32 * k_row_b + (uint32_t)g * 16;
+  // K and V tiles are both read row-coalesced: one load instruction covers
+  // 64 / CPR whole rows (a row is D * 2 contiguous bytes), which the memory
+  // pipeline serves as whole cache lines.  (Loading K straight in the MFMA
+  // operand layout touches 32 rows per instruction, 32 bytes each, and
+  // measured 11-20 % slower on this access pattern.)
+  const uint32_t k_voff = (uint32_t)(lane / CPR) * k_row_b + (uint32_t)(lane % CPR) * 16;
   const uint32_t v_voff = (uint32_t)(lane / CPR) * v_row_b + (uint32_t)(lane % CPR) * 16;
   // A tile past the split's end gets an empty resource: its loads return
   // zeros without touching memory or the block table.  Issuing every load
@@ -161,7 +176,8 @@ void decode_kernel(const DecodeParams p) {
     const auto rs = make_rsrc(live ? kg + tile_k(n0) : kg,
                               live ? rows_extent(0, L - n0, p.k_ss, D) : 0u);
 #pragma unroll
-    for (int kc = 0; kc < NKC; ++kc) kr_[kc] = buf_load16(rs, k_voff + kc * 32, 0);
+    for (int m = 0; m < VCH; ++m)
+      kr_[m] = buf_load16(rs, k_voff + (uint32_t)(m * (64 / CPR)) * k_row_b, 0);
   };
   u32x4 vreg[VCH];
   auto load_v = [&](int tt) {
@@ -180,11 +196,11 @@ void decode_kernel(const DecodeParams p) {
   float m_run = -INFINITY;
   float l_run = 0.f;
 
-  // One tile.  Two K register sets alternate (the set is refilled with tile
-  // tt + 2 * waves once its MFMAs are issued) and V's next load is issued as
-  // soon as this tile's V is in LDS, so each wave keeps about two tiles of
-  // loads in flight.
-  auto process = [&](int tt, u32x4* kr_) {
+  // One tile: the K and V registers (loaded one tile ahead) go to this
+  // wave's LDS slots, the next tile's loads are issued into the same
+  // registers, and the products run from LDS while those loads are in flight.
+  u32x4 kreg[VCH];
+  auto process = [&](int tt) {
     const int n0 = k_begin + tt * BN;
     // V tile -> this wave's LDS slot.  LDS executes one wave's instructions in
     // order, so the previous tile's transpose reads finished before these
@@ -193,17 +209,20 @@ void decode_kernel(const DecodeParams p) {
     for (int m = 0; m < VCH; ++m) {
       const int c = lane + 64 * m;
       store16(vslot + (c / CPR) * VSTR + (c % CPR) * 8, vreg[m]);
+      store16(kslot + k_lds_ofs(c / CPR, c % CPR), kreg[m]);
     }
     load_v(tt + kDecodeWaves);
+    load_k(tt + kDecodeWaves, kreg);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // S^T = K Q^T from the K registers, then refill the set.
+    // S^T = K Q^T: A = K rows from this wave's LDS slot (lane (c32, g) reads
+    // row c32, 16-dim step kc, half g).
     f32x16 s = f32x16{};
 #pragma unroll
-    for (int kc = 0; kc < NKC; ++kc) s = T::mfma32(kr_[kc], qreg[kc], s);
-    load_k(tt + 2 * kDecodeWaves, kr_);
+    for (int kc = 0; kc < NKC; ++kc)
+      s = T::mfma32(load16(kslot + k_lds_ofs(c32, 2 * kc + g)), qreg[kc], s);
 
     // Scores -> log2 units (GENERIC applies ALiBi first); mask keys outside
     // [key_lo, key_hi] (including rows past the sequence end).
@@ -257,16 +276,10 @@ void decode_kernel(const DecodeParams p) {
     }
   };
 
-  // Tiles w, w + 4, ... of the split; the second process() of an iteration
-  // may be past the end (all its keys masked: no contribution).
-  u32x4 kA[NKC], kB[NKC];
-  load_k(w, kA);
+  // Tiles w, w + 4, ... of the split.
+  load_k(w, kreg);
   load_v(w);
-  load_k(w + kDecodeWaves, kB);
-  for (int tt = w; tt < n_tiles; tt += 2 * kDecodeWaves) {
-    process(tt, kA);
-    process(tt + kDecodeWaves, kB);
-  }
+  for (int tt = w; tt < n_tiles; tt += kDecodeWaves) process(tt);
 
   // ------------------------------------------------------------ merge waves
   // LDS (after every wave's last V read): per wave w and row r, O^T values
@@ -276,7 +289,7 @@ void decode_kernel(const DecodeParams p) {
   float* mo = reinterpret_cast<float*>(smem);
   float* ml = mo + kDecodeWaves * 32 * D;
   const float l_w = halves_sum(l_run);
-  {
+  if (row_valid) {   // only the real rows are merged
     float* orow = mo + ((w * 32) + r) * D;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -354,7 +367,10 @@ void decode_kernel(const DecodeParams p) {
 // Merge the splits of each (b, query, head) row: out = sum_s exp(lse_s - lse)
 // o_s, lse = log sum_s exp(lse_s), over the splits that hold keys of that
 // sequence (ceil(L_b / split_keys); none -> out 0, lse -inf).  One thread per
-// row and 4 dims.
+// row and 4 dims.  The split LSEs and partial rows are fetched in batches of
+// kCombineBatch independent loads: a loop of dependent loads would pay one
+// memory latency per split.
+constexpr int kCombineBatch = 8;
 template <class T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams p, int head_dim) {
   const int quads = head_dim / 4;
@@ -368,19 +384,33 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams 
   const int b = (int)(row / ((int64_t)p.heads_q * p.seqlen_q));
   const int L = p.seqlens != nullptr ? p.seqlens[b] : p.max_keys;
   const int n = min(p.num_splits, (L + p.split_keys - 1) / p.split_keys);
-  float m = -INFINITY;
-  for (int s = 0; s < n; ++s) m = fmaxf(m, p.lse_part[(int64_t)s * nrows + row]);
+  // Running (max, sum, weighted rows) over batches of splits.
+  float m = -INFINITY, tot = 0.f;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  float tot = 0.f;
-  if (m != -INFINITY) {
-    for (int s = 0; s < n; ++s) {
-      const float ls = p.lse_part[(int64_t)s * nrows + row];
-      if (ls == -INFINITY) continue;
-      const float wgt = __expf(ls - m);
-      tot += wgt;
-      const f32x4 o = *reinterpret_cast<const f32x4*>(p.o_part + ((int64_t)s * nrows + row) * head_dim + qd * 4);
-      acc += wgt * o;
+  for (int s0 = 0; s0 < n; s0 += kCombineBatch) {
+    float ls[kCombineBatch];
+    f32x4 o[kCombineBatch];
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const int s = s0 + u;
+      ls[u] = s < n ? p.lse_part[(int64_t)s * nrows + row] : -INFINITY;
+      o[u] = s < n ? *reinterpret_cast<const f32x4*>(p.o_part + ((int64_t)s * nrows + row) * head_dim + qd * 4)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+    float mb = m;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) mb = fmaxf(mb, ls[u]);
+    if (mb == -INFINITY) continue;
+    const float rescale = __expf(m - mb);   // m == -inf -> 0
+    tot *= rescale;
+    acc *= rescale;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const float wgt = ls[u] == -INFINITY ? 0.f : __expf(ls[u] - mb);
+      tot += wgt;
+      acc += wgt * o[u];
+    }
+    m = mb;
   }
   const float inv = tot > 0.f ? 1.f / tot : 0.f;
   uint16_t* orow = static_cast<uint16_t*>(p.o) + (int64_t)b * p.o_sb + (int64_t)i * p.o_ss +
