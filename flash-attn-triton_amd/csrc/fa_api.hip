@@ -49,19 +49,26 @@ int clamp_window(int64_t w) {
 bool supported_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 
 // 16-byte vector loads need 16-byte aligned rows: base pointer aligned and
-// every stride a multiple of 8 two-byte elements.
-bool aligned16(const void* ptr, const int64_t* strides, int n) {
+// every stride a multiple of 16 bytes (8 two-byte or 4 four-byte elements).
+bool aligned16(const void* ptr, const int64_t* strides, int n, int64_t elem = 2) {
   if (reinterpret_cast<uintptr_t>(ptr) % 16 != 0) return false;
   for (int i = 0; i < n; ++i)
-    if (strides[i] % 8 != 0) return false;
+    if ((strides[i] * elem) % 16 != 0) return false;
   return true;
 }
 
 hipError_t launch_fwd(int dtype, const fa::FwdParams& p, int mode, int head_dim, bool generic,
                       hipStream_t st) {
+  if (dtype == FA_DTYPE_F32) return fa_launch_fwd_f32(p, mode, head_dim, generic, st);
   return dtype == FA_DTYPE_F16 ? fa_launch_fwd_f16(p, mode, head_dim, generic, st)
                                : fa_launch_fwd_bf16(p, mode, head_dim, generic, st);
 }
+
+bool supported_dtype(int dtype) {
+  return dtype == FA_DTYPE_F16 || dtype == FA_DTYPE_BF16 || dtype == FA_DTYPE_F32;
+}
+
+int64_t elem_bytes(int dtype) { return dtype == FA_DTYPE_F32 ? 4 : 2; }
 
 void fill_scale(fa::FwdParams& p, float scale, float softcap, const float* alibi) {
   p.scale = scale;
@@ -158,7 +165,7 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
   if (attn_bias && !bias_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_dense: attn_bias without bias_stride");
   if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_dense: lse without lse_stride");
-  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+  if (!supported_dtype(dtype))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: dtype %d not supported", dtype);
   if (!supported_head_dim(head_dim))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: head_dim %lld not in {16,32,64,128,256}",
@@ -171,10 +178,11 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
   if (seqlen_q > kMaxLen || seqlen_k > kMaxLen || q_pos_offset > kMaxLen ||
       q_pos_offset < -kMaxLen || batch * heads_q > INT32_MAX)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: sizes or position offset exceed 2^29");
-  if (!aligned16(q, q_stride, 3) || !aligned16(k, k_stride, 3) || !aligned16(v, v_stride, 3) ||
-      !aligned16(out, o_stride, 3))
+  const int64_t eb = elem_bytes(dtype);
+  if (!aligned16(q, q_stride, 3, eb) || !aligned16(k, k_stride, 3, eb) ||
+      !aligned16(v, v_stride, 3, eb) || !aligned16(out, o_stride, 3, eb))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_dense: tensors must be 16-byte aligned with strides "
-                                    "that are multiples of 8 elements");
+                                    "that are multiples of 16 bytes");
   if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
   fa::FwdParams p{};
   p.q = q; p.k = k; p.v = v; p.o = out; p.lse = lse;
@@ -215,7 +223,7 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
       !v_stride || !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_varlen: null pointer argument");
   if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_varlen: lse without lse_stride");
-  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+  if (!supported_dtype(dtype))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: dtype %d not supported", dtype);
   if (!supported_head_dim(head_dim))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: head_dim %lld not in {16,32,64,128,256}",
@@ -225,10 +233,11 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
     return fail(FA_ERR_INVALID, "fa_fwd_varlen: bad sizes");
   if (max_seqlen_q > kMaxLen || max_seqlen_k > kMaxLen || batch * heads_q > INT32_MAX)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: sizes exceed 2^29");
-  if (!aligned16(q, q_stride, 2) || !aligned16(k, k_stride, 2) || !aligned16(v, v_stride, 2) ||
-      !aligned16(out, o_stride, 2))
+  const int64_t eb = elem_bytes(dtype);
+  if (!aligned16(q, q_stride, 2, eb) || !aligned16(k, k_stride, 2, eb) ||
+      !aligned16(v, v_stride, 2, eb) || !aligned16(out, o_stride, 2, eb))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: tensors must be 16-byte aligned with strides "
-                                    "that are multiples of 8 elements");
+                                    "that are multiples of 16 bytes");
   if (batch == 0 || max_seqlen_q == 0) return hip_status(hipSuccess, "");
   fa::FwdParams p{};
   p.q = q; p.k = k; p.v = v; p.o = out; p.lse = lse;
@@ -286,7 +295,7 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
       !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: null pointer argument");
   if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_kvcache: lse without lse_stride");
-  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+  if (!supported_dtype(dtype))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: dtype %d not supported", dtype);
   if (!supported_head_dim(head_dim))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: head_dim %lld not supported",
@@ -298,10 +307,11 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: page_size must be positive");
   if (seqlen_q * (heads_q / heads_k) > kMaxLen || max_keys > kMaxLen)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: sizes exceed 2^29");
-  if (!aligned16(q, q_stride, 3) || !aligned16(k_cache, k_cache_stride, 3) ||
-      !aligned16(v_cache, v_cache_stride, 3) || !aligned16(out, o_stride, 3))
+  const int64_t eb = elem_bytes(dtype);
+  if (!aligned16(q, q_stride, 3, eb) || !aligned16(k_cache, k_cache_stride, 3, eb) ||
+      !aligned16(v_cache, v_cache_stride, 3, eb) || !aligned16(out, o_stride, 3, eb))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: tensors must be 16-byte aligned with "
-                                    "strides that are multiples of 8 elements");
+                                    "strides that are multiples of 16 bytes");
   const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
                                    block_table ? page_size : 0);
   if (num_splits != plan.num_splits)
@@ -313,7 +323,10 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     return fail(FA_ERR_INVALID, "fa_fwd_kvcache: workspace too small or misaligned (%lld < %lld)",
                 (long long)workspace_bytes, (long long)(plan.o_part_bytes + plan.lse_part_bytes));
   if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
-  if (plan.decode) {
+  // fp32 runs every key of a row in one workgroup: the plan's split count is
+  // checked above (the contract is dtype-independent) but no split is used.
+  const bool f32 = dtype == FA_DTYPE_F32;
+  if (plan.decode && !f32) {
     fa::DecodeParams d{};
     d.q = q; d.k = k_cache; d.v = v_cache; d.o = out; d.lse = lse;
     d.q_sb = q_stride[0]; d.q_ss = q_stride[1]; d.q_sh = q_stride[2];
@@ -358,15 +371,15 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
   p.seqlens_k = cache_seqlens;
   p.block_table = block_table; p.bt_stride = block_table_stride; p.page_size = (int)page_size;
   p.cache_rows = cache_batch_idx; p.leftpad = cache_leftpad;
-  p.num_splits = plan.num_splits; p.split_tiles = plan.split_tiles;
-  if (plan.num_splits > 1) {
+  p.num_splits = f32 ? 1 : plan.num_splits; p.split_tiles = plan.split_tiles;
+  if (p.num_splits > 1) {
     p.o_part = static_cast<float*>(workspace);
     p.lse_part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan.o_part_bytes);
   }
   p.heavy_first = 0;
   hipError_t e = launch_fwd(dtype, p, fa::kModeKvcache, (int)head_dim, needs_generic(p),
                             (hipStream_t)stream);
-  if (e == hipSuccess && plan.num_splits > 1)
+  if (e == hipSuccess && p.num_splits > 1)
     e = fa_launch_combine(dtype, p.o_part, p.lse_part, out, lse, plan.num_splits, (int)batch,
                           (int)seqlen_q, (int)heads_q, (int)head_dim, o_stride, lse_stride,
                           (hipStream_t)stream);
@@ -387,7 +400,7 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
     return fail(FA_ERR_INVALID, "fa_attn_probs: cu_seqlens_q and cu_seqlens_k go together");
   if (attn_bias && !bias_stride)
     return fail(FA_ERR_INVALID, "fa_attn_probs: attn_bias without bias_stride");
-  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+  if (!supported_dtype(dtype))
     return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: dtype %d not supported", dtype);
   if (!supported_head_dim(head_dim))
     return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: head_dim %lld not supported",
@@ -400,9 +413,9 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
     return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: lengths or offset exceed 2^29");
   if (max_seqlen_q > 4 * 65535)
     return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: max_seqlen_q above 262140 is not supported");
-  if (!aligned16(q, q_stride, 3) || !aligned16(k, k_stride, 3))
+  if (!aligned16(q, q_stride, 3, elem_bytes(dtype)) || !aligned16(k, k_stride, 3, elem_bytes(dtype)))
     return fail(FA_ERR_UNSUPPORTED, "fa_attn_probs: q/k must be 16-byte aligned with strides "
-                                    "that are multiples of 8 elements");
+                                    "that are multiples of 16 bytes");
   fa::ProbsParams p{};
   p.q = q; p.k = k; p.lse = lse; p.probs = probs; p.lse_out = lse_out;
   p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];

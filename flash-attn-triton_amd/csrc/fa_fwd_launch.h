@@ -167,6 +167,8 @@ hipError_t fa_launch_fwd_f16(const fa::FwdParams& p, int mode, int head_dim, boo
                              hipStream_t st);
 hipError_t fa_launch_fwd_bf16(const fa::FwdParams& p, int mode, int head_dim, bool generic,
                               hipStream_t st);
+hipError_t fa_launch_fwd_f32(const fa::FwdParams& p, int mode, int head_dim, bool generic,
+                             hipStream_t st);
 hipError_t fa_launch_combine(int dtype, const float* o_part, const float* lse_part, void* out,
                              float* lse, int num_splits, int batch, int seqlen_q, int heads,
                              int head_dim, const int64_t* o_stride, const int64_t* lse_stride,

@@ -13,13 +13,45 @@
 // [batch, heads_q, max_q] fp32 contiguous, -inf past q_len(b) (the padding of
 // the reference's varlen return, :644).  Rows whose LSE is -inf get all-zero
 // probabilities (nan_to_num of an empty softmax, :44).
+#include <type_traits>
+
 #include "fa_probs.h"
 #include "fa_common.h"
 
 namespace fa {
 
+// q . k over the head dim for 16-bit element types (T = F16 / BF16) or fp32
+// (T = float), accumulated in fp32.
+template <class T>
+__device__ inline float row_dot(const void* qv, const void* kv, int head_dim) {
+  float s = 0.f;
+  if constexpr (std::is_same<T, float>::value) {
+    const float* qp = static_cast<const float*>(qv);
+    const float* kp = static_cast<const float*>(kv);
+    for (int d = 0; d < head_dim; d += 4) {
+      const f32x4 qa = *reinterpret_cast<const f32x4*>(qp + d);
+      const f32x4 ka = *reinterpret_cast<const f32x4*>(kp + d);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s = fmaf(qa[e], ka[e], s);
+    }
+  } else {
+    const uint16_t* qp = static_cast<const uint16_t*>(qv);
+    const uint16_t* kp = static_cast<const uint16_t*>(kv);
+    for (int d = 0; d < head_dim; d += 8) {
+      const u32x4 qa = load16(qp + d), ka = load16(kp + d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int sh = (e & 1) * 16;
+        s = fmaf(T::to_float((uint16_t)(qa[e >> 1] >> sh)), T::to_float((uint16_t)(ka[e >> 1] >> sh)), s);
+      }
+    }
+  }
+  return s;
+}
+
 template <class T>
 __global__ __launch_bounds__(256) void probs_kernel(const ProbsParams p) {
+  constexpr int64_t kElem = std::is_same<T, float>::value ? 4 : 2;
   const int j = blockIdx.x * 64 + (threadIdx.x & 63);
   const int i = blockIdx.y * 4 + (threadIdx.x >> 6);
   const int bz = blockIdx.z;
@@ -49,17 +81,9 @@ __global__ __launch_bounds__(256) void probs_kernel(const ProbsParams p) {
   float lse = -INFINITY;
   if (i < Sq) lse = p.lse[lse_i + (int64_t)h * p.lse_sh];
   if (valid && lse != -INFINITY) {
-    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow + (int64_t)h * p.q_sh;
-    const uint16_t* kp = static_cast<const uint16_t*>(p.k) + krow + (int64_t)kvh * p.k_sh;
-    float s = 0.f;
-    for (int d = 0; d < p.head_dim; d += 8) {
-      const u32x4 qa = load16(qp + d), ka = load16(kp + d);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int sh = (e & 1) * 16;
-        s = fmaf(T::to_float((uint16_t)(qa[e >> 1] >> sh)), T::to_float((uint16_t)(ka[e >> 1] >> sh)), s);
-      }
-    }
+    const char* qp = static_cast<const char*>(p.q) + (qrow + (int64_t)h * p.q_sh) * kElem;
+    const char* kp = static_cast<const char*>(p.k) + (krow + (int64_t)kvh * p.k_sh) * kElem;
+    const float s = row_dot<T>(qp, kp, p.head_dim);
     const int qpos = i + (p.cu_q != nullptr ? 0 : p.q_offset);
     float x = s * p.scale;
     if (p.alibi != nullptr) x -= p.alibi[(int64_t)b * p.alibi_sb + h] * fabsf((float)(qpos - j));
@@ -86,7 +110,9 @@ hipError_t fa_launch_probs(int dtype, const fa::ProbsParams& p, hipStream_t st) 
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return hipSuccess;
   if (dtype == 0)
     hipLaunchKernelGGL(fa::probs_kernel<fa::F16>, grid, dim3(256), 0, st, p);
-  else
+  else if (dtype == 1)
     hipLaunchKernelGGL(fa::probs_kernel<fa::BF16>, grid, dim3(256), 0, st, p);
+  else
+    hipLaunchKernelGGL(fa::probs_kernel<float>, grid, dim3(256), 0, st, p);
   return hipGetLastError();
 }

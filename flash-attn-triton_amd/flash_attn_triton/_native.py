@@ -27,6 +27,7 @@ FA_ERR_UNSUPPORTED = 2
 FA_ERR_HIP = 3
 FA_DTYPE_F16 = 0
 FA_DTYPE_BF16 = 1
+FA_DTYPE_F32 = 2
 
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
@@ -111,7 +112,9 @@ def dtype_code(dtype: torch.dtype) -> int:
         return FA_DTYPE_F16
     if dtype == torch.bfloat16:
         return FA_DTYPE_BF16
-    raise RuntimeError(f"flash_attn_triton: the HIP kernels take fp16 or bf16, not {dtype}")
+    if dtype == torch.float32:
+        return FA_DTYPE_F32
+    raise RuntimeError(f"flash_attn_triton: the HIP kernels take fp16, bf16 or fp32, not {dtype}")
 
 
 def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offset: int,

@@ -12,7 +12,8 @@ defect or a host-side copy, never changes a correct result):
 * inputs are not padded to multiples of 64, grouped KV heads are never
   repeated, strided inputs are read in place: the kernels handle ragged
   lengths, GQA and BSHD strides directly;
-* bf16 inputs are accepted (the reference takes fp16/fp32 only);
+* bf16 inputs are accepted in addition to the reference's fp16 / fp32
+  (fp32 runs in fp32 throughout, on the fp32 matrix core);
 * ``flash_attn_with_kvcache`` runs one batched split-KV launch instead of a
   Python loop of gathers and O(L^2) padded launches, and its causal
   alignment is bottom-right for every cache length (the reference's dense
@@ -40,16 +41,6 @@ from . import _native
 from ._checks import Deferred
 
 BLOCK_SIZE = 64
-
-_FP32_MSG = (
-    "flash_attn_triton (gfx950 HIP build): fp32 inputs are not implemented by the HIP "
-    "kernels yet; pass fp16 or bf16 tensors")
-
-
-def _check_compute_dtype(dtype):
-    if dtype == torch.float32:
-        raise NotImplementedError(_FP32_MSG)
-
 
 def _normalize_alibi(alibi_slopes, batch, heads, device):
     """(H,) or (B,H) fp32 slopes -> contiguous (B,H) (flash_attn_interface.py:128-136)."""
@@ -99,7 +90,6 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     """
     if dropout_p > 0.0:
         raise NotImplementedError(DROPOUT_MSG)
-    _check_compute_dtype(q.dtype)
     batch, q_len, q_heads, head_dim = q.shape
     k_len = k.shape[1]
     if head_dim not in (16, 32, 64, 128, 256):
@@ -133,7 +123,6 @@ def _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen
     """
     if dropout_p > 0.0:
         raise NotImplementedError(DROPOUT_MSG)
-    _check_compute_dtype(q.dtype)
     batch = cu_seqlens_q.numel() - 1
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else softmax_scale
     out, lse_tok = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
@@ -223,7 +212,6 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
     assert head_dim in {16, 32, 64, 128, 256}
     if dropout_p > 0.0:
         raise NotImplementedError(DROPOUT_MSG)
-    _check_compute_dtype(q.dtype)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(head_dim)
     out = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
@@ -279,7 +267,6 @@ def flash_attn_func_cross(q, k, v, dropout_p=0.0, softmax_scale=None, causal=Fal
                                      causal_offset=_causal_offset)[0]
     if dropout_p > 0.0:
         raise NotImplementedError(DROPOUT_MSG)
-    _check_compute_dtype(q.dtype)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     out = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
@@ -414,8 +401,6 @@ def flash_attn_with_kvcache(
         chk.fail(ValueError("head dimension must be one of 16, 32, 64, 128, or 256"))
     if q.shape[2] % k_cache.shape[2] != 0:
         chk.fail(ValueError("The number of query heads must be divisible by KV heads"))
-    if q.dtype == torch.float32:
-        chk.fail(NotImplementedError(_FP32_MSG))
     if q.shape[0] == 0:
         chk.flush()
         return q.new_empty(q.shape)
@@ -539,8 +524,6 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                             window_size, softcap, alibi)
     if dropout_p > 0.0:
         chk.fail(NotImplementedError(DROPOUT_MSG))
-    if q.dtype == torch.float32:
-        chk.fail(NotImplementedError(_FP32_MSG))
     values = chk.flush()   # the one host synchronization of this call
     use_alibi = alibi is not None and bool(values[alibi_any])
     if softmax_scale is None:

@@ -53,10 +53,11 @@ def _wrap_grad(out: torch.Tensor, *inputs: torch.Tensor) -> torch.Tensor:
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
     """The kernels read rows with 16-byte loads: unit innermost stride, strides
-    that are multiples of 8 elements and a 16-byte aligned base.  Other layouts
+    that are multiples of 16 bytes and a 16-byte aligned base.  Other layouts
     get one contiguous copy (the reference copies every non-contiguous input,
     flash_attn_interface.py:202-204)."""
-    if (t.stride(-1) == 1 and all(s % 8 == 0 for s in t.stride()[:-1])
+    es = t.element_size()
+    if (t.stride(-1) == 1 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
             and t.data_ptr() % 16 == 0):
         return t
     return t.contiguous()

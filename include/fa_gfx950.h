@@ -11,8 +11,11 @@
  * forward path (cited per function); the Python layer of this package
  * (flash_attn_triton/) calls these through ctypes at exactly those sites.
  *
- * Tensor layouts.  `dtype` is FA_DTYPE_F16 or FA_DTYPE_BF16.  Strides are in
- * elements and the innermost (head-dim) stride must be 1.
+ * Tensor layouts.  `dtype` is FA_DTYPE_F16, FA_DTYPE_BF16 or FA_DTYPE_F32 (the
+ * reference accepts fp16 and fp32, flash_attn_interface.py:95-96; fp32 runs in
+ * fp32 throughout, on the fp32 matrix core; fa_quant_k_int8 / fa_fwd_int8 take
+ * fp16 only).  Strides are in elements and the innermost (head-dim) stride must
+ * be 1; rows must be 16-byte aligned.
  */
 #ifndef FA_GFX950_H_
 #define FA_GFX950_H_
@@ -32,6 +35,7 @@ typedef struct ihipStream_t* fa_stream_t; /* == hipStream_t */
 
 #define FA_DTYPE_F16 0
 #define FA_DTYPE_BF16 1
+#define FA_DTYPE_F32 2
 
 /* Library version (major*10000 + minor*100 + patch). */
 int fa_version(void);
