@@ -12,6 +12,7 @@
 #include "fa_gfx950.h"
 #include "fa_decode.h"
 #include "fa_probs.h"
+#include "fa_kvappend.h"
 #include "fa_fwd_launch.h"
 
 namespace {
@@ -435,6 +436,71 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
   p.window_left = clamp_window(window_left);
   p.window_right = clamp_window(window_right);
   return hip_status(fa_launch_probs(dtype, p, (hipStream_t)stream), "fa_attn_probs launch");
+}
+
+int fa_kvcache_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                      const int32_t* cache_seqlens, const int32_t* block_table,
+                      int64_t block_table_stride, int64_t page_size, int64_t num_pages,
+                      const int32_t* cache_batch_idx, int64_t cache_rows,
+                      const int32_t* cache_leftpad, int64_t capacity, const float* rotary_cos,
+                      const float* rotary_sin, int64_t rotary_dim, int64_t rotary_rows,
+                      int rotary_interleaved, int64_t batch, int64_t n_new, int64_t heads_k,
+                      int64_t head_dim, const int64_t* k_new_stride, const int64_t* v_new_stride,
+                      const int64_t* k_cache_stride, const int64_t* v_cache_stride, int dtype,
+                      fa_stream_t stream) {
+  if (!k_new || !v_new || !k_cache || !v_cache || !k_new_stride || !v_new_stride ||
+      !k_cache_stride || !v_cache_stride)
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: null pointer argument");
+  if (!supported_dtype(dtype))
+    return fail(FA_ERR_UNSUPPORTED, "fa_kvcache_append: dtype %d not supported", dtype);
+  if (batch < 0 || n_new < 0 || heads_k <= 0 || head_dim <= 0 || capacity < 0 ||
+      (block_table && (page_size <= 0 || num_pages <= 0)) || (!block_table && cache_rows <= 0))
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: bad sizes");
+  if ((rotary_cos == nullptr) != (rotary_sin == nullptr))
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: rotary_cos and rotary_sin go together");
+  if (rotary_cos && (rotary_dim <= 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim ||
+                     rotary_rows <= 0))
+    return fail(FA_ERR_INVALID, "fa_kvcache_append: rotary_dim %lld must be even, positive and "
+                                "at most head_dim", (long long)rotary_dim);
+  if (batch * n_new * heads_k * head_dim > INT64_C(1) << 40 || capacity > kMaxLen)
+    return fail(FA_ERR_UNSUPPORTED, "fa_kvcache_append: sizes too large");
+  fa::AppendParams p{};
+  p.k_new = k_new; p.v_new = v_new; p.k_cache = k_cache; p.v_cache = v_cache;
+  p.kn_sb = k_new_stride[0]; p.kn_ss = k_new_stride[1]; p.kn_sh = k_new_stride[2];
+  p.vn_sb = v_new_stride[0]; p.vn_ss = v_new_stride[1]; p.vn_sh = v_new_stride[2];
+  p.kc_sb = k_cache_stride[0]; p.kc_ss = k_cache_stride[1]; p.kc_sh = k_cache_stride[2];
+  p.vc_sb = v_cache_stride[0]; p.vc_ss = v_cache_stride[1]; p.vc_sh = v_cache_stride[2];
+  p.seqlens = cache_seqlens; p.block_table = block_table; p.bt_stride = block_table_stride;
+  p.page_size = (int)page_size; p.num_pages = (int)num_pages;
+  p.cache_rows = cache_batch_idx; p.cache_rows_n = (int)cache_rows; p.leftpad = cache_leftpad;
+  p.capacity = capacity;
+  p.cos = rotary_cos; p.sin = rotary_sin; p.rot = (int)rotary_dim;
+  p.interleaved = rotary_interleaved != 0; p.table_rows = rotary_rows;
+  p.batch = (int)batch; p.n_new = (int)n_new; p.heads_k = (int)heads_k; p.head_dim = (int)head_dim;
+  return hip_status(fa_launch_kv_append(dtype, p, (hipStream_t)stream), "fa_kvcache_append launch");
+}
+
+int fa_rotary_q(const void* q, void* out, const int32_t* cache_seqlens,
+                const int32_t* cache_leftpad, const float* rotary_cos, const float* rotary_sin,
+                int64_t rotary_dim, int64_t rotary_rows, int rotary_interleaved, int64_t batch,
+                int64_t seqlen_q, int64_t heads, int64_t head_dim, const int64_t* q_stride,
+                const int64_t* out_stride, int dtype, fa_stream_t stream) {
+  if (!q || !out || !cache_seqlens || !rotary_cos || !rotary_sin || !q_stride || !out_stride)
+    return fail(FA_ERR_INVALID, "fa_rotary_q: null pointer argument");
+  if (!supported_dtype(dtype))
+    return fail(FA_ERR_UNSUPPORTED, "fa_rotary_q: dtype %d not supported", dtype);
+  if (batch < 0 || seqlen_q < 0 || heads <= 0 || head_dim <= 0 || rotary_rows <= 0 ||
+      rotary_dim <= 0 || rotary_dim % 2 != 0 || rotary_dim > head_dim)
+    return fail(FA_ERR_INVALID, "fa_rotary_q: bad sizes");
+  fa::RotaryQParams p{};
+  p.q = q; p.out = out;
+  p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];
+  p.o_sb = out_stride[0]; p.o_ss = out_stride[1]; p.o_sh = out_stride[2];
+  p.seqlens = cache_seqlens; p.leftpad = cache_leftpad;
+  p.cos = rotary_cos; p.sin = rotary_sin; p.rot = (int)rotary_dim;
+  p.interleaved = rotary_interleaved != 0; p.table_rows = rotary_rows;
+  p.batch = (int)batch; p.seqlen_q = (int)seqlen_q; p.heads = (int)heads; p.head_dim = (int)head_dim;
+  return hip_status(fa_launch_rotary_q(dtype, p, (hipStream_t)stream), "fa_rotary_q launch");
 }
 
 int fa_quant_k_int8(const void* k, int8_t* k8, float* s_k, int64_t batch, int64_t heads,

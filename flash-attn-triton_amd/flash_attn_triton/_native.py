@@ -54,6 +54,11 @@ _SIGNATURES = {
     "fa_attn_probs": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64, _i64,
                              _f32, _vp, _i64, _vp, _i64p, _vp]),
+    "fa_kvcache_append": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp,
+                                 _i64, _vp, _vp, _i64, _i64, _int, _i64, _i64, _i64, _i64,
+                                 _i64p, _i64p, _i64p, _i64p, _int, _vp]),
+    "fa_rotary_q": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _i64, _i64,
+                           _i64, _i64p, _i64p, _int, _vp]),
     "fa_quant_k_int8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _vp]),
     "fa_fwd_int8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p,
                            _i64p, _f32, _int, _i64, _i64, _vp]),
@@ -221,6 +226,40 @@ def fwd_kvcache(q, k_cache, v_cache, out, lse, cache_seqlens, block_table, cache
         0 if alibi is None else int(alibi.stride(0)), splits, _ptr(workspace),
         int(ws_bytes), _stream(q.device))
     _check(status, "fa_fwd_kvcache")
+
+
+def kvcache_append(k_new, v_new, k_cache, v_cache, cache_seqlens, block_table, cache_batch_idx,
+                   cache_leftpad, capacity: int, rotary_cos, rotary_sin,
+                   rotary_interleaved: bool) -> None:
+    """Write k_new / v_new [B, n, Hk, D] into the cache in place (see fa_kvcache_append)."""
+    lib = load()
+    B, n, Hk, D = k_new.shape
+    paged = block_table is not None
+    rot = 2 * rotary_cos.shape[-1] if rotary_cos is not None else 0
+    status = lib.fa_kvcache_append(
+        _ptr(k_new), _ptr(v_new), _ptr(k_cache), _ptr(v_cache), _ptr(cache_seqlens),
+        _ptr(block_table), int(block_table.stride(0)) if paged else 0,
+        int(k_cache.shape[1]) if paged else 0, int(k_cache.shape[0]) if paged else 0,
+        _ptr(cache_batch_idx), 0 if paged else int(k_cache.shape[0]), _ptr(cache_leftpad),
+        int(capacity), _ptr(rotary_cos), _ptr(rotary_sin), rot,
+        int(rotary_cos.shape[0]) if rotary_cos is not None else 0, int(bool(rotary_interleaved)),
+        B, n, Hk, D, _strides(k_new.stride()[:3]), _strides(v_new.stride()[:3]),
+        _strides(k_cache.stride()[:3]), _strides(v_cache.stride()[:3]), dtype_code(k_new.dtype),
+        _stream(k_new.device))
+    _check(status, "fa_kvcache_append")
+
+
+def rotary_q(q, out, cache_seqlens, cache_leftpad, rotary_cos, rotary_sin,
+             rotary_interleaved: bool) -> None:
+    """out = q rotated at positions cache_seqlens[b] - Sq + leftpad[b] + i (see fa_rotary_q)."""
+    lib = load()
+    B, Sq, H, D = q.shape
+    status = lib.fa_rotary_q(
+        _ptr(q), _ptr(out), _ptr(cache_seqlens), _ptr(cache_leftpad), _ptr(rotary_cos),
+        _ptr(rotary_sin), 2 * rotary_cos.shape[-1], int(rotary_cos.shape[0]),
+        int(bool(rotary_interleaved)), B, Sq, H, D, _strides(q.stride()[:3]),
+        _strides(out.stride()[:3]), dtype_code(q.dtype), _stream(q.device))
+    _check(status, "fa_rotary_q")
 
 
 def quant_k_int8(k, k8, s_k) -> None:

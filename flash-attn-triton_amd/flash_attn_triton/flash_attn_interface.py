@@ -380,23 +380,56 @@ def flash_attn_with_kvcache(
         if leftpads.numel():
             chk.check((leftpads < 0).any(), bad_pads)
     zero_pad = 0 if leftpads is None else leftpads
-    if k is not None or v is not None:
-        chk.fail(NotImplementedError(
-            "flash_attn_triton (gfx950 HIP build): appending k/v to the cache is not "
-            "implemented yet"))
+    cos_t = sin_t = None
     if rotary_cos is not None:
-        chk.fail(NotImplementedError(
-            "flash_attn_triton (gfx950 HIP build): rotary embedding in "
-            "flash_attn_with_kvcache is not implemented yet"))
-    if cache_seqlens is None:
-        lengths = torch.full((q.shape[0],), cache_capacity, dtype=torch.int64, device=q.device)
+        # The reference casts the tables to the input dtype before rotating
+        # (flash_attn_interface.py:56-57); the kernels then rotate in fp32.
+        if rotary_cos.ndim != 2 or rotary_sin.shape != rotary_cos.shape:
+            chk.fail(ValueError("rotary_cos and rotary_sin must be (seqlen_ro, rotary_dim / 2) "
+                                "tables of the same shape"))
+        if rotary_cos.shape[-1] * 2 > q.shape[-1]:
+            chk.fail(ValueError("rotary tables exceed the head dimension"))
+        cos_t = rotary_cos.to(device=q.device).to(q.dtype).float().contiguous()
+        sin_t = rotary_sin.to(device=q.device).to(q.dtype).float().contiguous()
+    bad_rotary = IndexError("rotary position out of range of the cos/sin tables")
+    n_new = 0
+    if k is not None or v is not None:
+        # Append (reference :468-493), performed in place on the cache.
+        if k is None or v is None or k.shape != v.shape:
+            chk.fail(ValueError("k and v must be supplied together with matching shapes"))
+        if k.shape[0] != q.shape[0] or k.shape[2:] != k_cache.shape[2:]:
+            chk.fail(ValueError("new k/v tensors are incompatible with the cache"))
+        n_new = k.shape[1]
+        if cache_seqlens is None:
+            lengths = torch.zeros(q.shape[0], dtype=torch.int64, device=q.device)
+        else:
+            lengths = torch.as_tensor(cache_seqlens, device=q.device, dtype=torch.int64).flatten()
+        bad_fit = ValueError("new KV tensors do not fit in the cache")
+        if lengths.numel() != q.shape[0]:
+            chk.fail(bad_fit)
+        if lengths.numel():
+            chk.check((lengths < 0).any() | (lengths + zero_pad + n_new > cache_capacity).any(),
+                      bad_fit)
+        if cos_t is not None and lengths.numel() and n_new:
+            chk.check((lengths + zero_pad + n_new > cos_t.shape[0]).any(), bad_rotary)
     else:
-        lengths = torch.as_tensor(cache_seqlens, device=q.device, dtype=torch.int64).flatten()
-    bad_lengths = ValueError("cache_seqlens must contain valid lengths for every batch item")
-    if lengths.numel() != q.shape[0]:
-        chk.fail(bad_lengths)
-    if lengths.numel():
-        chk.check((lengths < 0).any() | (lengths + zero_pad > cache_capacity).any(), bad_lengths)
+        if cache_seqlens is None:
+            lengths = torch.full((q.shape[0],), cache_capacity, dtype=torch.int64, device=q.device)
+        else:
+            lengths = torch.as_tensor(cache_seqlens, device=q.device, dtype=torch.int64).flatten()
+        bad_lengths = ValueError("cache_seqlens must contain valid lengths for every batch item")
+        if lengths.numel() != q.shape[0]:
+            chk.fail(bad_lengths)
+        if lengths.numel():
+            chk.check((lengths < 0).any() | (lengths + zero_pad > cache_capacity).any(),
+                      bad_lengths)
+    if cos_t is not None and lengths.numel() and q.shape[1]:
+        # Query rows rotate at L + leftpad - Sq + i (L after the append);
+        # negative positions index from the end of the tables, as torch
+        # indexing does in the reference (:516-517).
+        first = lengths + n_new + zero_pad - q.shape[1]
+        chk.check((first + q.shape[1] > cos_t.shape[0]).any() | (first < -cos_t.shape[0]).any(),
+                  bad_rotary)
     if q.shape[-1] not in (16, 32, 64, 128, 256):
         chk.fail(ValueError("head dimension must be one of 16, 32, 64, 128, or 256"))
     if q.shape[2] % k_cache.shape[2] != 0:
@@ -415,14 +448,26 @@ def flash_attn_with_kvcache(
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     from .triton_kernel.attention_kernel import _kernel_ready
+    lengths32 = lengths.to(torch.int32).contiguous()
+    bt32 = block_table.to(device=q.device, dtype=torch.int32).contiguous() if paged else None
+    rows32 = cache_rows.to(torch.int32).contiguous() if cache_rows is not None else None
+    pads32 = leftpads.to(torch.int32).contiguous() if leftpads is not None else None
+    if n_new:
+        kn = k.to(device=q.device, dtype=k_cache.dtype)
+        vn = v.to(device=q.device, dtype=v_cache.dtype)
+        _native.kvcache_append(kn, vn, k_cache, v_cache, lengths32, bt32, rows32, pads32,
+                               int(cache_capacity), cos_t, sin_t, rotary_interleaved)
+        lengths32 = (lengths32 + n_new).to(torch.int32)
     qk = _kernel_ready(q)
+    if cos_t is not None and q.shape[1]:
+        q_rot = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        _native.rotary_q(q, q_rot, lengths32, pads32, cos_t, sin_t, rotary_interleaved)
+        qk = q_rot
     kc, vc = _kernel_ready(k_cache), _kernel_ready(v_cache)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     _native.fwd_kvcache(
-        qk, kc, vc, out, None, lengths.to(torch.int32).contiguous(),
-        block_table.to(device=q.device, dtype=torch.int32).contiguous() if paged else None,
-        cache_rows.to(torch.int32).contiguous() if cache_rows is not None else None,
-        leftpads.to(torch.int32).contiguous() if leftpads is not None else None,
+        qk, kc, vc, out, None, lengths32,
+        bt32, rows32, pads32,
         int(cache_capacity), softmax_scale, causal, window_size[0], window_size[1], alibi)
     return _wrap_grad(out, q)
 

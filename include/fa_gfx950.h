@@ -164,6 +164,45 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
                   const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
                   const int64_t* bias_stride, fa_stream_t stream);
 
+/* KV-cache append, the cache write of flash_attn_with_kvcache(k=, v=, ...)
+ * (replaces the reference's append at flash_attn_interface.py:468-493, which
+ * writes into an advanced-indexing copy and is lost; here the cache is
+ * written in place, as upstream FlashAttention-2 does).  Token t of batch b
+ * (k_new/v_new [batch, n_new, heads_k, head_dim]) goes to logical position
+ * pos = cache_seqlens[b] + cache_leftpad[b] + t (cache_seqlens / cache_leftpad
+ * nullable = 0): slot pos % page_size of page block_table[b*block_table_stride
+ * + pos/page_size] (paged, num_pages pages), else position pos of cache row
+ * cache_batch_idx[b] (nullable = b; cache_rows rows of capacity positions).
+ * With rotary_cos/rotary_sin (fp32 [rotary_rows, rotary_dim/2], row-major,
+ * already rounded to the element type) k is rotated at position pos before the
+ * write (flash_attn_interface.py:52-66: interleaved pairs (2j, 2j+1) or
+ * half-split pairs (j, j + rotary_dim/2); dims past rotary_dim are copied).
+ * Positions outside [0, capacity), pages outside [0, num_pages) and rows
+ * outside the tables are skipped (the caller validates them first). */
+int fa_kvcache_append(const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                      const int32_t* cache_seqlens, const int32_t* block_table,
+                      int64_t block_table_stride, int64_t page_size, int64_t num_pages,
+                      const int32_t* cache_batch_idx, int64_t cache_rows,
+                      const int32_t* cache_leftpad, int64_t capacity, const float* rotary_cos,
+                      const float* rotary_sin, int64_t rotary_dim, int64_t rotary_rows,
+                      int rotary_interleaved, int64_t batch, int64_t n_new, int64_t heads_k,
+                      int64_t head_dim, const int64_t* k_new_stride, const int64_t* v_new_stride,
+                      const int64_t* k_cache_stride, const int64_t* v_cache_stride, int dtype,
+                      fa_stream_t stream);
+
+/* Rotary embedding of the queries of flash_attn_with_kvcache(rotary_cos=...)
+ * (replaces flash_attn_interface.py:515-518): out[b][i][h] = q[b][i][h] rotated
+ * at position cache_seqlens[b] - seqlen_q + cache_leftpad[b] + i, where
+ * cache_seqlens holds the lengths after any append; a negative position
+ * counts from the end of the tables (torch indexing in the reference); tables
+ * and pairing as in fa_kvcache_append.  q and out are
+ * [batch, seqlen_q, heads, head_dim]. */
+int fa_rotary_q(const void* q, void* out, const int32_t* cache_seqlens,
+                const int32_t* cache_leftpad, const float* rotary_cos, const float* rotary_sin,
+                int64_t rotary_dim, int64_t rotary_rows, int rotary_interleaved, int64_t batch,
+                int64_t seqlen_q, int64_t heads, int64_t head_dim, const int64_t* q_stride,
+                const int64_t* out_stride, int dtype, fa_stream_t stream);
+
 /* Per-token INT8 quantization of K (fp16), bit-exact with
  * `_quantize_k_rows` (attention_kernel_int8.py:58-79, launched at :232):
  *   s = fp32(max(amax_row, 1)) / 127;  k8 = round_half_away(fp32(k) * (1/s)).
