@@ -219,10 +219,15 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   const int64_t* v_stride, const int64_t* o_stride, const int64_t* lse_stride,
                   int dtype, float softmax_scale, int causal, int64_t window_left,
                   int64_t window_right, float softcap, const float* alibi_slopes,
-                  int64_t alibi_batch_stride, fa_stream_t stream) {
+                  int64_t alibi_batch_stride, const int32_t* seqused_q,
+                  const int32_t* seqused_k, const int32_t* cu_seqlens_out,
+                  const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
+                  fa_stream_t stream) {
   if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k || !q_stride || !k_stride ||
       !v_stride || !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_varlen: null pointer argument");
+  if (block_table && page_size <= 0)
+    return fail(FA_ERR_INVALID, "fa_fwd_varlen: page_size must be positive with a block table");
   if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_varlen: lse without lse_stride");
   if (!supported_dtype(dtype))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: dtype %d not supported", dtype);
@@ -235,19 +240,27 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
   if (max_seqlen_q > kMaxLen || max_seqlen_k > kMaxLen || batch * heads_q > INT32_MAX)
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: sizes exceed 2^29");
   const int64_t eb = elem_bytes(dtype);
-  if (!aligned16(q, q_stride, 2, eb) || !aligned16(k, k_stride, 2, eb) ||
-      !aligned16(v, v_stride, 2, eb) || !aligned16(out, o_stride, 2, eb))
+  const int nkv = block_table ? 3 : 2;   // paged K/V: {page, slot, head} strides
+  if (!aligned16(q, q_stride, 2, eb) || !aligned16(k, k_stride, nkv, eb) ||
+      !aligned16(v, v_stride, nkv, eb) || !aligned16(out, o_stride, 2, eb))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: tensors must be 16-byte aligned with strides "
                                     "that are multiples of 16 bytes");
   if (batch == 0 || max_seqlen_q == 0) return hip_status(hipSuccess, "");
   fa::FwdParams p{};
   p.q = q; p.k = k; p.v = v; p.o = out; p.lse = lse;
   p.q_ss = q_stride[0]; p.q_sh = q_stride[1];
-  p.k_ss = k_stride[0]; p.k_sh = k_stride[1];
-  p.v_ss = v_stride[0]; p.v_sh = v_stride[1];
+  if (block_table) {
+    p.k_sb = k_stride[0]; p.k_ss = k_stride[1]; p.k_sh = k_stride[2];
+    p.v_sb = v_stride[0]; p.v_ss = v_stride[1]; p.v_sh = v_stride[2];
+    p.block_table = block_table; p.bt_stride = block_table_stride; p.page_size = (int)page_size;
+  } else {
+    p.k_ss = k_stride[0]; p.k_sh = k_stride[1];
+    p.v_ss = v_stride[0]; p.v_sh = v_stride[1];
+  }
   p.o_ss = o_stride[0]; p.o_sh = o_stride[1];
   if (lse) { p.lse_ss = lse_stride[0]; p.lse_sh = lse_stride[1]; }
   p.cu_q = cu_seqlens_q; p.cu_k = cu_seqlens_k;
+  p.seqused_q = seqused_q; p.seqused_k = seqused_k; p.cu_o = cu_seqlens_out;
   p.batch = (int)batch; p.seqlen_q = (int)max_seqlen_q; p.seqlen_k = (int)max_seqlen_k;
   p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
   fill_scale(p, softmax_scale, softcap, alibi_slopes);

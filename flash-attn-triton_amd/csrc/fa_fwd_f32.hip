@@ -89,11 +89,18 @@ void fwd_f32_kernel(const FwdParams p) {
       const int qs = p.cu_q[b], ks = p.cu_k[b];
       Sq = p.cu_q[b + 1] - qs;
       Sk = p.cu_k[b + 1] - ks;
+      if (p.seqused_q != nullptr) Sq = max(0, min(Sq, p.seqused_q[b]));
+      if (p.seqused_k != nullptr) Sk = max(0, min(Sk, p.seqused_k[b]));
+      const int os = p.cu_o != nullptr ? p.cu_o[b] : qs;
       q_base = (int64_t)qs * p.q_ss;
-      o_base = (int64_t)qs * p.o_ss;
-      lse_base = (int64_t)qs * p.lse_ss;
-      k_base = (int64_t)ks * p.k_ss;
-      v_base = (int64_t)ks * p.v_ss;
+      o_base = (int64_t)os * p.o_ss;
+      lse_base = (int64_t)os * p.lse_ss;
+      if (p.block_table != nullptr) {
+        bt_row = p.block_table + (int64_t)b * p.bt_stride;   // paged varlen
+      } else {
+        k_base = (int64_t)ks * p.k_ss;
+        v_base = (int64_t)ks * p.v_ss;
+      }
     } else {
       Sq = p.seqlen_q;
       Sk = p.seqlen_k;
@@ -177,7 +184,7 @@ void fwd_f32_kernel(const FwdParams p) {
   }
 
   auto key_offset = [&](int j, int64_t base, int64_t sb, int64_t ss) -> int64_t {
-    if (MODE == kModeKvcache && bt_row != nullptr) {
+    if (bt_row != nullptr) {
       const int page = bt_row[j / p.page_size];
       return base + (int64_t)page * sb + (int64_t)(j % p.page_size) * ss;
     }

@@ -117,6 +117,11 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
 template <class T, int D, int MODE, bool GEN>
 hipError_t launch_fwd_d(const FwdParams& p, hipStream_t st) {
   if (MODE == kModePrefill) {
+    // Paged varlen keys need a page lookup per key: the general kernel.
+    if (p.block_table != nullptr) {
+      using C = PrefillCfg<D>;
+      return launch_fwd_cfg<T, D, C::NW, C::BN, MODE, GEN>(p, p.seqlen_q, p.heads_q * p.batch, st);
+    }
     if constexpr (D % 32 == 0) {
       return launch_prefill<T, D, GEN>(p, st);
     } else {

@@ -101,9 +101,12 @@ void prefill_kernel(const FwdParams p) {
     const int qs = p.cu_q[b], ks = p.cu_k[b];
     Sq = p.cu_q[b + 1] - qs;
     Sk = p.cu_k[b + 1] - ks;
+    if (p.seqused_q != nullptr) Sq = max(0, min(Sq, p.seqused_q[b]));
+    if (p.seqused_k != nullptr) Sk = max(0, min(Sk, p.seqused_k[b]));
+    const int os = p.cu_o != nullptr ? p.cu_o[b] : qs;
     q_base = (int64_t)qs * p.q_ss;
-    o_base = (int64_t)qs * p.o_ss;
-    lse_base = (int64_t)qs * p.lse_ss;
+    o_base = (int64_t)os * p.o_ss;
+    lse_base = (int64_t)os * p.lse_ss;
     k_base = (int64_t)ks * p.k_ss;
     v_base = (int64_t)ks * p.v_ss;
   } else {

@@ -46,7 +46,7 @@ _SIGNATURES = {
                             _i64, _f32, _vp, _i64, _vp, _i64p, _vp]),
     "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
-                             _i64, _f32, _vp, _i64, _vp]),
+                             _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
     "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
     "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
@@ -175,20 +175,26 @@ def attn_probs(q, k, lse, probs, lse_out, cu_q, cu_k, max_seqlen_q: int, max_seq
 
 def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
                softmax_scale: float, causal: bool, window_left: int, window_right: int,
-               softcap: float, alibi) -> None:
-    """q [Tq,Hq,D], k/v [Tk,Hk,D]; cu_* int32 [batch+1]; lse [Tq,Hq] or None."""
+               softcap: float, alibi, seqused_q=None, seqused_k=None, cu_out=None,
+               block_table=None) -> None:
+    """q [Tq,Hq,D], k/v [Tk,Hk,D] (or paged [pages,page,Hk,D] with block_table);
+    cu_* int32 [batch+1]; lse [Tout,Hq] or None; see fa_fwd_varlen."""
     lib = load()
     Hq, D = q.shape[1], q.shape[2]
-    Hk = k.shape[1]
+    paged = block_table is not None
+    Hk = k.shape[2] if paged else k.shape[1]
+    nkv = 3 if paged else 2
     batch = cu_q.numel() - 1
     lse_stride = _strides(lse.stride()) if lse is not None else None
     status = lib.fa_fwd_varlen(
         _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(lse), _ptr(cu_q), _ptr(cu_k), batch,
         int(max_seqlen_q), int(max_seqlen_k), Hq, Hk, D, _strides(q.stride()[:2]),
-        _strides(k.stride()[:2]), _strides(v.stride()[:2]), _strides(out.stride()[:2]),
+        _strides(k.stride()[:nkv]), _strides(v.stride()[:nkv]), _strides(out.stride()[:2]),
         lse_stride, dtype_code(q.dtype), float(softmax_scale), int(bool(causal)),
         int(window_left), int(window_right), float(softcap), _ptr(alibi),
-        0 if alibi is None else int(alibi.stride(0)), _stream(q.device))
+        0 if alibi is None else int(alibi.stride(0)), _ptr(seqused_q), _ptr(seqused_k),
+        _ptr(cu_out), _ptr(block_table), int(block_table.stride(0)) if paged else 0,
+        int(k.shape[1]) if paged else 0, _stream(q.device))
     _check(status, "fa_fwd_varlen")
 
 

@@ -23,6 +23,7 @@ defect or a host-side copy, never changes a correct result):
 """
 from __future__ import annotations
 
+import itertools
 import math
 from typing import Optional
 
@@ -472,6 +473,47 @@ def flash_attn_with_kvcache(
     return _wrap_grad(out, q)
 
 
+def _packed_index(starts, lengths, device):
+    """Row indices ``starts[b] + [0, lengths[b])`` concatenated over b (host lists)."""
+    parts = [torch.arange(s, s + n, device=device) for s, n in zip(starts, lengths) if n > 0]
+    return torch.cat(parts) if parts else torch.zeros((0,), dtype=torch.long, device=device)
+
+
+def _compact_varlen(q, k, v, cu_q, cu_k, used_q, used_k, block_table):
+    """Gathered ``(q, k, v, cu_q, cu_k)`` holding only the used rows of every
+    sequence and the keys of a paged cache in order; the reference builds its
+    inputs this way (flash_attn_interface.py:533-581).  Only the
+    ``return_attn_probs`` path, which materialises probabilities anyway, uses
+    it: the kernels read seqused_* and the block table directly."""
+    dev = q.device
+    cq, ck = cu_q.tolist(), cu_k.tolist()
+    lq = [b - a for a, b in zip(cq[:-1], cq[1:])]
+    lk = [b - a for a, b in zip(ck[:-1], ck[1:])]
+    uq = used_q.tolist() if used_q is not None else lq
+    uk = used_k.tolist() if used_k is not None else lk
+    if block_table is not None:
+        page = k.shape[1]
+        bt = block_table.to(device=dev, dtype=torch.long)
+        parts = []
+        for b, n in enumerate(uk):
+            if n > 0:
+                j = torch.arange(n, device=dev)
+                parts.append(bt[b, j // page] * page + j % page)
+        idx = torch.cat(parts) if parts else torch.zeros((0,), dtype=torch.long, device=dev)
+        k = k.reshape(-1, k.shape[2], k.shape[3])[idx]
+        v = v.reshape(-1, v.shape[2], v.shape[3])[idx]
+    elif used_k is not None:
+        idx = _packed_index(ck[:-1], uk, dev)
+        k, v = k[idx], v[idx]
+    if used_q is not None:
+        q = q[_packed_index(cq[:-1], uq, dev)]
+
+    def prefix(lengths):
+        return torch.tensor([0] + list(itertools.accumulate(lengths)), dtype=torch.int32,
+                            device=dev)
+    return q, k, v, prefix(uq), prefix(uk)
+
+
 def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                            max_seqlen_k, dropout_p=0.0, softmax_scale=None, causal=False,
                            window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
@@ -481,46 +523,84 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
 
     q: (total_q, nheads, headdim), k/v: (total_k, nheads_k, headdim),
     cu_seqlens_*: (batch + 1,) int32 prefix sums.  Returns (total_q, nheads, headdim).
+
+    block_table (batch, max_pages) int32 makes k / v paged caches
+    (num_pages, page_size, nheads_k, headdim): key j of sequence b sits in
+    slot j % page_size of page block_table[b, j // page_size], and
+    cu_seqlens_k only gives the key counts.  seqused_q / seqused_k (batch,)
+    keep the first seqused_*[b] queries / keys of sequence b; the output
+    then packs the used queries only (sum(seqused_q) rows), as the
+    reference's compaction does (:551-581).  The kernels read the block
+    table and the used counts directly: nothing is gathered or copied.
     """
-    if block_table is not None:
+    batch_size = cu_seqlens_q.numel() - 1
+    chk = Deferred()
+    paged = block_table is not None
+    if paged:
         if k.ndim != 4 or v.ndim != 4 or k.shape != v.shape:
             raise ValueError("paged varlen k and v must have shape (pages, page_size, heads, dim)")
         if block_table.ndim != 2 or block_table.shape[0] != cu_seqlens_k.numel() - 1:
             raise ValueError("block_table must have shape (batch, max_num_pages)")
         page_size = k.shape[1]
         lengths_k = (cu_seqlens_k[1:] - cu_seqlens_k[:-1]).to(torch.long)
-        page_counts = (lengths_k + page_size - 1) // page_size
-        cols = torch.arange(block_table.shape[1], device=block_table.device)
-        used = cols[None, :] < page_counts[:, None].to(block_table.device)
-        used_ids = block_table[used].to(torch.long)
-        if torch.any(used_ids < 0) or torch.any(used_ids >= k.shape[0]):
-            raise ValueError("block_table contains an invalid physical page index")
-        raise NotImplementedError(
-            "flash_attn_triton (gfx950 HIP build): paged varlen prefill "
-            "(block_table in flash_attn_varlen_func) is not implemented yet")
-    batch_size = cu_seqlens_q.numel() - 1
-    if seqused_q is not None or seqused_k is not None:
-        raise NotImplementedError(
-            "flash_attn_triton (gfx950 HIP build): seqused_q / seqused_k are not implemented yet")
-    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3 or k.shape != v.shape:
-        raise ValueError("packed q, k, and v must be rank-3 tensors with matching KV shapes")
+        page_counts = torch.div(lengths_k + page_size - 1, page_size, rounding_mode="floor")
+        bt_long = block_table.to(device=cu_seqlens_k.device, dtype=torch.long)
+        cols = torch.arange(block_table.shape[1], device=cu_seqlens_k.device)
+        used_pages = cols[None, :] < page_counts[:, None]
+        chk.check((((bt_long < 0) | (bt_long >= k.shape[0])) & used_pages).any(),
+                  ValueError("block_table contains an invalid physical page index"))
+        # Keys past the table's last page do not exist: the reference's gather
+        # comes up short and its size check below fails.
+        paged_short = (lengths_k > block_table.shape[1] * page_size).any()
+    if seqused_q is not None:
+        seqused_q = torch.as_tensor(seqused_q, device=q.device, dtype=torch.int64).flatten()
+        if seqused_q.numel() != batch_size:
+            chk.fail(ValueError("seqused_q must contain one value per sequence"))
+        seqused_q = seqused_q.to(cu_seqlens_q.device)
+        lengths_q = (cu_seqlens_q[1:] - cu_seqlens_q[:-1]).to(torch.long)
+        chk.check(((seqused_q < 0) | (seqused_q > lengths_q)).any(),
+                  ValueError("seqused_q exceeds the packed query sequence"))
+    if seqused_k is not None:
+        seqused_k = torch.as_tensor(seqused_k, device=k.device, dtype=torch.int64).flatten()
+        if seqused_k.numel() != batch_size:
+            chk.fail(ValueError("seqused_k must contain one value per sequence"))
+        seqused_k = seqused_k.to(cu_seqlens_k.device)
+        lengths_k = (cu_seqlens_k[1:] - cu_seqlens_k[:-1]).to(torch.long)
+        chk.check(((seqused_k < 0) | (seqused_k > lengths_k)).any(),
+                  ValueError("seqused_k exceeds the packed KV sequence"))
+    if q.ndim != 3 or (not paged and (k.ndim != 3 or v.ndim != 3 or k.shape != v.shape)):
+        chk.fail(ValueError("packed q, k, and v must be rank-3 tensors with matching KV shapes"))
     if cu_seqlens_q.ndim != 1 or cu_seqlens_k.ndim != 1:
-        raise ValueError("cu_seqlens arrays must be one-dimensional")
+        chk.fail(ValueError("cu_seqlens arrays must be one-dimensional"))
     if cu_seqlens_q.numel() != cu_seqlens_k.numel():
-        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same batch size")
-    chk = Deferred()
+        chk.fail(ValueError("cu_seqlens_q and cu_seqlens_k must describe the same batch size"))
     bad_start = ValueError("cu_seqlens arrays must start at zero and contain a batch boundary")
     if cu_seqlens_q.numel() == 0:
-        raise bad_start
-    chk.check(cu_seqlens_q[0] != 0, bad_start)
-    chk.check(cu_seqlens_k[0] != 0, bad_start)
+        chk.fail(bad_start)
+    # With seqused_* the reference re-derives that side's cu_seqlens from the
+    # used counts (:563, :581), so its start/order/size checks always pass.
+    if seqused_q is None:
+        chk.check(cu_seqlens_q[0] != 0, bad_start)
+    if seqused_k is None:
+        chk.check(cu_seqlens_k[0] != 0, bad_start)
     if cu_seqlens_q.numel() > 1:
         bad_order = ValueError("cu_seqlens arrays must be monotonically non-decreasing")
-        chk.check((cu_seqlens_q[1:] < cu_seqlens_q[:-1]).any(), bad_order)
-        chk.check((cu_seqlens_k[1:] < cu_seqlens_k[:-1]).any(), bad_order)
+        if seqused_q is None:
+            chk.check((cu_seqlens_q[1:] < cu_seqlens_q[:-1]).any(), bad_order)
+        if seqused_k is None:
+            chk.check((cu_seqlens_k[1:] < cu_seqlens_k[:-1]).any(), bad_order)
     bad_size = ValueError("cu_seqlens values exceed the packed tensor sizes")
-    chk.check(cu_seqlens_q[-1] > q.shape[0], bad_size)
-    chk.check(cu_seqlens_k[-1] > k.shape[0], bad_size)
+    if seqused_q is None:
+        chk.check(cu_seqlens_q[-1] > q.shape[0], bad_size)
+    else:
+        chk.check((cu_seqlens_q[:-1] + seqused_q > q.shape[0]).any(), bad_size)
+    if paged:
+        chk.check(paged_short, bad_size)
+    elif seqused_k is None:
+        chk.check(cu_seqlens_k[-1] > k.shape[0], bad_size)
+    else:
+        chk.check((cu_seqlens_k[:-1] + seqused_k > k.shape[0]).any(), bad_size)
+    kv_heads = k.shape[-2]
     if (q.dtype not in (torch.float16, torch.bfloat16, torch.float32) or k.dtype != q.dtype
             or v.dtype != q.dtype):
         chk.fail(ValueError(
@@ -533,7 +613,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         chk.fail(ValueError("q, k, and v must have the same head dimension"))
     if q.shape[-1] not in (16, 32, 64, 128, 256):
         chk.fail(ValueError("head dimension must be one of 16, 32, 64, 128, or 256"))
-    if q.shape[1] % k.shape[1] != 0:
+    if q.shape[1] % kv_heads != 0:
         chk.fail(ValueError("The number of query heads must be divisible by KV heads"))
     if dropout_p < 0.0 or dropout_p >= 1.0:
         chk.fail(ValueError("dropout_p must be in the range [0, 1)"))
@@ -546,17 +626,28 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     cu_seqlens_k = cu_seqlens_k.to(dtype=torch.int32).contiguous()
     if max_seqlen_q < 0 or max_seqlen_k < 0:
         chk.fail(ValueError("max sequence lengths must be non-negative"))
-    bad_cover = ValueError("cu_seqlens arrays must cover the packed q and KV tensors")
-    chk.check(cu_seqlens_q[-1] != q.shape[0], bad_cover)
-    chk.check(cu_seqlens_k[-1] != k.shape[0], bad_cover)
+    if not paged:
+        # A paged k has exactly the keys cu_seqlens_k names once the size
+        # check above passed; seqused_* sides are covered by construction.
+        bad_cover = ValueError("cu_seqlens arrays must cover the packed q and KV tensors")
+        if seqused_q is None:
+            chk.check(cu_seqlens_q[-1] != q.shape[0], bad_cover)
+        if seqused_k is None:
+            chk.check(cu_seqlens_k[-1] != k.shape[0], bad_cover)
+    elif seqused_q is None:
+        chk.check(cu_seqlens_q[-1] != q.shape[0],
+                  ValueError("cu_seqlens arrays must cover the packed q and KV tensors"))
     if cu_seqlens_q.numel() < 2:
         chk.fail(ValueError("cu_seqlens arrays must describe at least one sequence"))
-    chk.check(((cu_seqlens_q[1:] - cu_seqlens_q[:-1]).max() > max_seqlen_q) |
-              ((cu_seqlens_k[1:] - cu_seqlens_k[:-1]).max() > max_seqlen_k),
+    used_len_q = seqused_q if seqused_q is not None else cu_seqlens_q[1:] - cu_seqlens_q[:-1]
+    used_len_k = seqused_k if seqused_k is not None else cu_seqlens_k[1:] - cu_seqlens_k[:-1]
+    chk.check((used_len_q.max() > max_seqlen_q) | (used_len_k.max() > max_seqlen_k),
               ValueError("max sequence lengths must cover every packed sequence"))
+    out_rows = chk.value(seqused_q.sum()) if seqused_q is not None else None
     if max_seqlen_q == 0 or max_seqlen_k == 0:
-        chk.flush()
-        return q.new_zeros((q.shape[0], q.shape[1], q.shape[2]))
+        values = chk.flush()
+        rows = values[out_rows] if out_rows is not None else q.shape[0]
+        return q.new_zeros((rows, q.shape[1], q.shape[2]))
     try:
         alibi = _normalize_alibi(alibi_slopes, batch_size, q.shape[1], q.device)
     except ValueError as exc:
@@ -564,6 +655,9 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
     if return_attn_probs:
         chk.flush()
+        if paged or seqused_q is not None or seqused_k is not None:
+            q, k, v, cu_seqlens_q, cu_seqlens_k = _compact_varlen(
+                q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_q, seqused_k, block_table)
         return _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                             max_seqlen_k, dropout_p, softmax_scale, causal,
                                             window_size, softcap, alibi)
@@ -573,10 +667,17 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     use_alibi = alibi is not None and bool(values[alibi_any])
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
+    cu_out = None
+    if seqused_q is not None:
+        cu_out = torch.zeros((batch_size + 1,), dtype=torch.int32, device=q.device)
+        torch.cumsum(seqused_q, 0, out=cu_out[1:])
     out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                          softmax_scale=softmax_scale, causal=causal,
                          window_left=window_size[0], window_right=window_size[1],
-                         softcap=softcap, alibi=alibi if use_alibi else None)
+                         softcap=softcap, alibi=alibi if use_alibi else None,
+                         seqused_q=seqused_q, seqused_k=seqused_k,
+                         out_rows=values[out_rows] if out_rows is not None else None,
+                         cu_out=cu_out, block_table=block_table)
     return _wrap_grad(out, q, k, v)
 
 

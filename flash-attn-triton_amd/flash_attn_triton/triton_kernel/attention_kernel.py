@@ -88,18 +88,32 @@ def dense_forward(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: 
 def varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
                    softmax_scale: float, causal: bool, window_left: int = -1,
                    window_right: int = -1, softcap: float = 0.0,
-                   alibi: Optional[torch.Tensor] = None, return_lse: bool = False):
-    """Run the packed varlen HIP kernel on ``[T, H, D]`` tensors."""
+                   alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
+                   seqused_q: Optional[torch.Tensor] = None,
+                   seqused_k: Optional[torch.Tensor] = None,
+                   out_rows: Optional[int] = None, cu_out: Optional[torch.Tensor] = None,
+                   block_table: Optional[torch.Tensor] = None):
+    """Run the packed varlen HIP kernel on ``[T, H, D]`` tensors.
+
+    ``seqused_q``/``seqused_k`` limit each sequence to its first queries /
+    keys; with ``cu_out`` the outputs of the used queries are packed into
+    ``out_rows`` rows (sequence b at ``cu_out[b]``).  With ``block_table``
+    k / v are paged caches ``[pages, page_size, Hk, D]``."""
+    dev = q.device
     qk, kk, vk = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v)
-    out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    lse = (torch.empty((q.shape[0], q.shape[1]), dtype=torch.float32, device=q.device)
+    rows = q.shape[0] if out_rows is None else int(out_rows)
+    out = torch.empty((rows, q.shape[1], q.shape[2]), dtype=q.dtype, device=dev)
+    lse = (torch.empty((rows, q.shape[1]), dtype=torch.float32, device=dev)
            if return_lse else None)
     if alibi is not None:
-        alibi = alibi.to(device=q.device, dtype=torch.float32).contiguous()
-    cu_q = cu_q.to(device=q.device, dtype=torch.int32).contiguous()
-    cu_k = cu_k.to(device=q.device, dtype=torch.int32).contiguous()
-    _native.fwd_varlen(qk, kk, vk, out, lse, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
-                       softmax_scale, causal, window_left, window_right, softcap, alibi)
+        alibi = alibi.to(device=dev, dtype=torch.float32).contiguous()
+
+    def i32(t):
+        return None if t is None else t.to(device=dev, dtype=torch.int32).contiguous()
+
+    _native.fwd_varlen(qk, kk, vk, out, lse, i32(cu_q), i32(cu_k), max_seqlen_q, max_seqlen_k,
+                       softmax_scale, causal, window_left, window_right, softcap, alibi,
+                       i32(seqused_q), i32(seqused_k), i32(cu_out), i32(block_table))
     return (out, lse) if return_lse else out
 
 

@@ -83,6 +83,18 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
  * entries); positions are local to each sequence.  max_seqlen_q must bound
  * every query length.  lse (nullable) is [Tq, Hq] at
  * lse[t*lse_stride[0] + h*lse_stride[1]].  Other arguments as fa_fwd_dense.
+ *
+ * seqused_q / seqused_k (nullable, int32 [batch]; flash_attn_interface.py:551-580)
+ * limit sequence b to its first seqused_q[b] queries / seqused_k[b] keys
+ * (0 <= used <= length, checked by the caller).  cu_seqlens_out (nullable,
+ * int32 [batch+1]) places sequence b's output and LSE rows at
+ * [cu_seqlens_out[b], ...) instead of cu_seqlens_q[b] (the reference packs the
+ * outputs of the used queries).  block_table (nullable; int32
+ * [batch, block_table_stride]) makes k/v paged caches [pages, page_size, Hk, D]
+ * with *_stride[3] = {page, slot, head}: key j of sequence b is slot
+ * j % page_size of page block_table[b][j / page_size], the length of sequence
+ * b still being cu_seqlens_k[b+1] - cu_seqlens_k[b] (paged varlen prefill,
+ * flash_attn_interface.py:533-550, without the reference's gather).
  */
 int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float* lse,
                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
@@ -91,7 +103,10 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   const int64_t* v_stride, const int64_t* o_stride, const int64_t* lse_stride,
                   int dtype, float softmax_scale, int causal, int64_t window_left,
                   int64_t window_right, float softcap, const float* alibi_slopes,
-                  int64_t alibi_batch_stride, fa_stream_t stream);
+                  int64_t alibi_batch_stride, const int32_t* seqused_q,
+                  const int32_t* seqused_k, const int32_t* cu_seqlens_out,
+                  const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
+                  fa_stream_t stream);
 
 /* Split-KV plan for fa_fwd_kvcache: the number of key splits the launch will
  * use and the workspace bytes it needs (0 when num_splits == 1).

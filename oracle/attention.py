@@ -38,6 +38,7 @@ __all__ = [
     "attention_varlen",
     "attention_kvcache",
     "gather_paged_kv",
+    "compact_varlen",
     "apply_rotary",
 ]
 
@@ -161,6 +162,43 @@ def gather_paged_kv(cache, block_table_row, length: int, start: int = 0) -> np.n
     pages = np.asarray(block_table_row[:n_pages], dtype=np.int64)
     flat = cache[pages].reshape(-1, cache.shape[2], cache.shape[3])
     return flat[start:start + length]
+
+
+def compact_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_q=None, seqused_k=None,
+                   block_table=None):
+    """The reference's input rewrite for paged / partially used varlen
+    sequences (``flash_attn_interface.py:533-581``), in its order:
+
+    1. ``block_table`` given: ``k, v [pages, page_size, Hk, D]`` become packed
+       ``[sum(len_k), Hk, D]`` by gathering each sequence's first
+       ``ceil(len_k / page_size)`` pages and keeping ``len_k`` rows
+       (``:538-550``), ``len_k = cu_k[b+1] - cu_k[b]``;
+    2. ``seqused_q``: sequence b keeps its first ``seqused_q[b]`` queries and
+       ``cu_q`` is rebuilt from the used counts (``:551-563``);
+    3. ``seqused_k``: the same for keys and values (``:564-581``).
+
+    Returns ``(q, k, v, cu_q, cu_k)`` ready for :func:`attention_varlen`.
+    """
+    q, k, v = np.asarray(q), np.asarray(k), np.asarray(v)
+    cu_q = [int(x) for x in np.asarray(cu_seqlens_q)]
+    cu_k = [int(x) for x in np.asarray(cu_seqlens_k)]
+    batch = len(cu_q) - 1
+    if block_table is not None:
+        bt = np.asarray(block_table)
+        kp = [gather_paged_kv(k, bt[b], cu_k[b + 1] - cu_k[b]) for b in range(batch)]
+        vp = [gather_paged_kv(v, bt[b], cu_k[b + 1] - cu_k[b]) for b in range(batch)]
+        k = np.concatenate(kp) if kp else k[:0, 0]
+        v = np.concatenate(vp) if vp else v[:0, 0]
+    if seqused_q is not None:
+        used = [int(x) for x in np.asarray(seqused_q)]
+        q = np.concatenate([q[cu_q[b]:cu_q[b] + used[b]] for b in range(batch)])
+        cu_q = [0] + list(np.cumsum(used))
+    if seqused_k is not None:
+        used = [int(x) for x in np.asarray(seqused_k)]
+        k = np.concatenate([k[cu_k[b]:cu_k[b] + used[b]] for b in range(batch)])
+        v = np.concatenate([v[cu_k[b]:cu_k[b] + used[b]] for b in range(batch)])
+        cu_k = [0] + list(np.cumsum(used))
+    return q, k, v, np.asarray(cu_q, dtype=np.int64), np.asarray(cu_k, dtype=np.int64)
 
 
 def apply_rotary(x, cos, sin, positions, interleaved: bool) -> np.ndarray:

@@ -234,6 +234,49 @@ def test_paged_gather_is_the_contiguous_sequence():
     np.testing.assert_array_equal(ora.gather_paged_kv(cache, perm, L), contiguous)
 
 
+def test_compact_varlen_paged_rebuilds_the_packed_keys():
+    # Sequences written token by token into shuffled pages come back packed.
+    rng = np.random.default_rng(42)
+    page, lengths = 4, [5, 0, 9]
+    packed = rng.standard_normal((sum(lengths), 2, 8))
+    cache = rng.standard_normal((8, page, 2, 8))
+    perm = rng.permutation(8)
+    bt = np.zeros((3, 3), dtype=np.int64)
+    used, start = 0, 0
+    for b, L in enumerate(lengths):
+        n = (L + page - 1) // page
+        bt[b, :n] = perm[used:used + n]
+        for t in range(L):
+            cache[bt[b, t // page], t % page] = packed[start + t]
+        used += n
+        start += L
+    cu = np.array([0, 5, 5, 14])
+    q = rng.standard_normal((3, 2, 8))
+    _, k, v, cu_q, cu_k = ora.compact_varlen(q, cache, cache, [0, 1, 2, 3], cu, block_table=bt)
+    np.testing.assert_array_equal(k, packed)
+    np.testing.assert_array_equal(cu_k, cu)
+
+
+def test_compact_varlen_seqused_is_truncated_per_sequence_sdpa():
+    # seqused keeps each sequence's first rows: the result is SDPA of the
+    # truncated slices, concatenated; full counts change nothing.
+    lq, lk, uq, uk = [4, 6, 3], [5, 7, 2], [2, 6, 0], [5, 3, 1]
+    cq, ck = np.cumsum([0] + lq), np.cumsum([0] + lk)
+    q, k, v = _rand((13, 2, 8), 43), _rand((14, 2, 8), 44), _rand((14, 2, 8), 45)
+    cq2, ck2 = ora.compact_varlen(q, k, v, cq, ck, lq, lk)[3:]
+    np.testing.assert_array_equal(cq2, cq)
+    np.testing.assert_array_equal(ck2, ck)
+    out, _ = ora.attention_varlen(*ora.compact_varlen(q, k, v, cq, ck, uq, uk), causal=True)
+    exp = []
+    for b in range(3):
+        qb = q[None, cq[b]:cq[b] + uq[b]]
+        if uq[b] == 0:
+            continue
+        exp.append(_sdpa(qb, k[None, ck[b]:ck[b] + uk[b]], v[None, ck[b]:ck[b] + uk[b]], True)[0])
+    np.testing.assert_allclose(out, np.concatenate(exp), atol=1e-12)
+    assert out.shape[0] == sum(uq)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_kvcache_decode_matches_sdpa_bottom_right(causal):
     rng = np.random.default_rng(41)
