@@ -14,6 +14,7 @@
 #include "fa_probs.h"
 #include "fa_kvappend.h"
 #include "fa_fwd_launch.h"
+#include "fa_bwd.h"
 
 namespace {
 
@@ -147,6 +148,47 @@ hipError_t fa_launch_combine(int dtype, const float* o_part, const float* lse_pa
   return hipGetLastError();
 }
 
+namespace {
+
+// Shared part of fa_bwd_dense / fa_bwd_varlen: checks, scale fields, launch.
+int bwd_launch(const char* name, fa::BwdParams& p, int dtype, int64_t head_dim,
+               float softmax_scale, float softcap, const float* alibi_slopes,
+               int64_t alibi_batch_stride, int causal, int64_t window_left, int64_t window_right,
+               hipStream_t st) {
+  p.scale = softmax_scale;
+  p.scale_log2 = softmax_scale * fa::kLog2e;
+  p.softcap = softcap;
+  p.softcap_k = softcap > 0.f ? 2.f * fa::kLog2e / softcap : 0.f;
+  p.alibi = alibi_slopes;
+  p.alibi_sb = alibi_batch_stride;
+  p.causal = causal != 0;
+  p.window_left = clamp_window(window_left);
+  p.window_right = clamp_window(window_right);
+  const bool generic = alibi_slopes != nullptr || softcap > 0.f;
+  const hipError_t e = dtype == FA_DTYPE_F16 ? fa_launch_bwd_f16(p, (int)head_dim, generic, st)
+                                             : fa_launch_bwd_bf16(p, (int)head_dim, generic, st);
+  return hip_status(e, name);
+}
+
+int bwd_check_common(const char* name, const void* q, const void* k, const void* v,
+                     const void* out, const void* dout, const float* lse, const void* dq,
+                     const void* dk, const void* dv, const float* delta, int dtype,
+                     int64_t head_dim, int64_t heads_q, int64_t heads_k) {
+  if (!q || !k || !v || !out || !dout || !lse || !dq || !dk || !dv || !delta)
+    return fail(FA_ERR_INVALID, "%s: null pointer argument", name);
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
+    return fail(FA_ERR_UNSUPPORTED, "%s: dtype %d not supported (fp16 / bf16)", name, dtype);
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(FA_ERR_UNSUPPORTED, "%s: head_dim %lld not in {32,64,128,256}", name,
+                (long long)head_dim);
+  if (heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0)
+    return fail(FA_ERR_INVALID, "%s: bad head counts Hq=%lld Hk=%lld", name, (long long)heads_q,
+                (long long)heads_k);
+  return FA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int fa_version(void) { return 100; }
@@ -273,6 +315,99 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
   return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim, needs_generic(p),
                                (hipStream_t)stream),
                     "fa_fwd_varlen launch");
+}
+
+int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                 const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
+                 int64_t seqlen_q, int64_t seqlen_k, int64_t heads_q, int64_t heads_k,
+                 int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                 const int64_t* v_stride, const int64_t* o_stride, const int64_t* do_stride,
+                 const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
+                 const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                 int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
+                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream) {
+  const char* name = "fa_bwd_dense";
+  int rc = bwd_check_common(name, q, k, v, out, dout, lse, dq, dk, dv, delta, dtype, head_dim,
+                            heads_q, heads_k);
+  if (rc != FA_OK) return rc;
+  if (!q_stride || !k_stride || !v_stride || !o_stride || !do_stride || !dq_stride ||
+      !dk_stride || !dv_stride || !lse_stride)
+    return fail(FA_ERR_INVALID, "%s: null stride argument", name);
+  if (batch < 0 || seqlen_q < 0 || seqlen_k < 0)
+    return fail(FA_ERR_INVALID, "%s: bad sizes B=%lld Sq=%lld Sk=%lld", name, (long long)batch,
+                (long long)seqlen_q, (long long)seqlen_k);
+  if (seqlen_q > kMaxLen || seqlen_k > kMaxLen || q_pos_offset > kMaxLen ||
+      q_pos_offset < -kMaxLen || batch * heads_q > INT32_MAX)
+    return fail(FA_ERR_UNSUPPORTED, "%s: sizes or position offset exceed 2^29", name);
+  if (!aligned16(q, q_stride, 3) || !aligned16(k, k_stride, 3) || !aligned16(v, v_stride, 3) ||
+      !aligned16(out, o_stride, 3) || !aligned16(dout, do_stride, 3) ||
+      !aligned16(dq, dq_stride, 3) || !aligned16(dk, dk_stride, 3) || !aligned16(dv, dv_stride, 3))
+    return fail(FA_ERR_UNSUPPORTED, "%s: tensors must be 16-byte aligned with strides that are "
+                                    "multiples of 16 bytes", name);
+  if (batch == 0) return hip_status(hipSuccess, "");
+  fa::BwdParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = out; p.dout = dout; p.dq = dq; p.dk = dk; p.dv = dv;
+  p.lse = lse; p.delta = delta;
+  p.q_sb = q_stride[0]; p.q_ss = q_stride[1]; p.q_sh = q_stride[2];
+  p.k_sb = k_stride[0]; p.k_ss = k_stride[1]; p.k_sh = k_stride[2];
+  p.v_sb = v_stride[0]; p.v_ss = v_stride[1]; p.v_sh = v_stride[2];
+  p.o_sb = o_stride[0]; p.o_ss = o_stride[1]; p.o_sh = o_stride[2];
+  p.do_sb = do_stride[0]; p.do_ss = do_stride[1]; p.do_sh = do_stride[2];
+  p.dq_sb = dq_stride[0]; p.dq_ss = dq_stride[1]; p.dq_sh = dq_stride[2];
+  p.dk_sb = dk_stride[0]; p.dk_ss = dk_stride[1]; p.dk_sh = dk_stride[2];
+  p.dv_sb = dv_stride[0]; p.dv_ss = dv_stride[1]; p.dv_sh = dv_stride[2];
+  p.lse_sb = lse_stride[0]; p.lse_sh = lse_stride[1]; p.lse_ss = lse_stride[2];
+  p.batch = (int)batch; p.seqlen_q = (int)seqlen_q; p.seqlen_k = (int)seqlen_k;
+  p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
+  p.q_offset = q_pos_offset;
+  return bwd_launch(name, p, dtype, head_dim, softmax_scale, softcap, alibi_slopes,
+                    alibi_batch_stride, causal, window_left, window_right, (hipStream_t)stream);
+}
+
+int fa_bwd_varlen(const void* q, const void* k, const void* v, const void* out,
+                  const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t heads_q, int64_t heads_k,
+                  int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride, const int64_t* do_stride,
+                  const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
+                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                  int64_t window_left, int64_t window_right, float softcap,
+                  const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream) {
+  const char* name = "fa_bwd_varlen";
+  int rc = bwd_check_common(name, q, k, v, out, dout, lse, dq, dk, dv, delta, dtype, head_dim,
+                            heads_q, heads_k);
+  if (rc != FA_OK) return rc;
+  if (!cu_seqlens_q || !cu_seqlens_k || !q_stride || !k_stride || !v_stride || !o_stride ||
+      !do_stride || !dq_stride || !dk_stride || !dv_stride || !lse_stride)
+    return fail(FA_ERR_INVALID, "%s: null pointer argument", name);
+  if (batch < 0 || max_seqlen_q < 0 || max_seqlen_k < 0)
+    return fail(FA_ERR_INVALID, "%s: bad sizes", name);
+  if (max_seqlen_q > kMaxLen || max_seqlen_k > kMaxLen || batch * heads_q > INT32_MAX)
+    return fail(FA_ERR_UNSUPPORTED, "%s: sizes exceed 2^29", name);
+  if (!aligned16(q, q_stride, 2) || !aligned16(k, k_stride, 2) || !aligned16(v, v_stride, 2) ||
+      !aligned16(out, o_stride, 2) || !aligned16(dout, do_stride, 2) ||
+      !aligned16(dq, dq_stride, 2) || !aligned16(dk, dk_stride, 2) || !aligned16(dv, dv_stride, 2))
+    return fail(FA_ERR_UNSUPPORTED, "%s: tensors must be 16-byte aligned with strides that are "
+                                    "multiples of 16 bytes", name);
+  if (batch == 0) return hip_status(hipSuccess, "");
+  fa::BwdParams p{};
+  p.q = q; p.k = k; p.v = v; p.o = out; p.dout = dout; p.dq = dq; p.dk = dk; p.dv = dv;
+  p.lse = lse; p.delta = delta;
+  p.q_ss = q_stride[0]; p.q_sh = q_stride[1];
+  p.k_ss = k_stride[0]; p.k_sh = k_stride[1];
+  p.v_ss = v_stride[0]; p.v_sh = v_stride[1];
+  p.o_ss = o_stride[0]; p.o_sh = o_stride[1];
+  p.do_ss = do_stride[0]; p.do_sh = do_stride[1];
+  p.dq_ss = dq_stride[0]; p.dq_sh = dq_stride[1];
+  p.dk_ss = dk_stride[0]; p.dk_sh = dk_stride[1];
+  p.dv_ss = dv_stride[0]; p.dv_sh = dv_stride[1];
+  p.lse_ss = lse_stride[0]; p.lse_sh = lse_stride[1];
+  p.cu_q = cu_seqlens_q; p.cu_k = cu_seqlens_k;
+  p.batch = (int)batch; p.seqlen_q = (int)max_seqlen_q; p.seqlen_k = (int)max_seqlen_k;
+  p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
+  return bwd_launch(name, p, dtype, head_dim, softmax_scale, softcap, alibi_slopes,
+                    alibi_batch_stride, causal, window_left, window_right, (hipStream_t)stream);
 }
 
 int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,

@@ -1,0 +1,611 @@
+// FlashAttention-2 backward for gfx950, fp16 / bf16 inputs, fp32 accumulation.
+//
+// Gradients of the forward in fa_prefill_kernel.h, following the reference's
+// backward (/root/reference/flash_attn_triton/triton_kernel/attention_kernel.py:
+// 536-566 `_attn_bwd_preprocess`, :569-668 `_attn_bwd_dkdv`, :671-776
+// `_attn_bwd_dq`, :809-1054 `_attn_bwd`; varlen :107-272):
+//   P  = exp(s - lse)        s = scale * q.k  -> ALiBi -> softcap -> mask
+//   dV = P^T dO              dP = dO V^T       delta = rowsum(dO * O)
+//   dS = P * (dP - delta) * softcap'          (softcap' = 1 - tanh^2, else 1)
+//   dQ = scale * dS K        dK = scale * dS^T Q
+// with the forward's natural-log LSE, so P is exactly the forward's
+// probabilities (rows with no visible key have LSE = -inf and P = 0).
+//
+// Two kernels, no atomics, deterministic:
+// * bwd_dq_kernel: a workgroup owns BM = 32*NW query rows of one (batch,
+//   head); wave w owns 32 rows and keeps Q and dO of its rows in VGPRs.  Per
+//   tile of BN keys: S^T = K Q^T and dP^T = V dO^T (A = K / V rows from LDS,
+//   B = Q^T / dO^T from VGPRs), dS^T in registers, dQ^T += K^T dS^T (A = K^T
+//   by the LDS transpose read).  The accumulator layouts put one query row in
+//   each lane, so LSE and delta are per-lane scalars and dS^T is already the
+//   B operand of the dQ^T product (the same key permutation as the forward's
+//   P^T).  It also writes delta, computed from its dO and O rows.
+// * bwd_dkdv_kernel: a workgroup owns BN = 32*NW keys of one (batch, KV
+//   head); wave w owns 32 keys and keeps K and V of its keys in VGPRs.  Per
+//   tile of BM query rows (of every query head of the GQA group, so each dK /
+//   dV element has one writer): S = Q K^T, dP = dO V^T (A = Q / dO rows from
+//   LDS), P and dS in registers with one key per lane, dV^T += dO^T P and
+//   dK^T += Q^T dS (A = dO^T / Q^T by the transpose read).
+// Every LDS tile is read both row-wise (16-byte reads of one row per lane)
+// and transposed (ds_read_b64_tr_b16), so tiles are stored unpadded with an
+// XOR swizzle of their 16-byte chunks (swz_off) that keeps both patterns free
+// of bank conflicts.
+#pragma once
+
+#include "fa_bwd.h"
+#include "fa_common.h"
+
+namespace fa {
+
+// Element offset of 16-byte chunk c of row r in a swizzled tile whose rows
+// hold D 16-bit elements.  Chunks are grouped into 256-byte lines (the width
+// of the 64 LDS banks); within a line the chunk position is XORed with a
+// function of the line.  Row reads (16 lanes, 16 consecutive rows, one chunk
+// each) and transpose reads (4 consecutive rows x 4 consecutive chunks per 16
+// lanes) both land on 16 distinct chunk positions.
+template <int D>
+__device__ inline int swz_off(int r, int c) {
+  constexpr int CPR = D / 8;
+  if constexpr (CPR >= 16) {
+    const int line = r * (CPR / 16) + (c >> 4);
+    const int s = ((r & 3) << 2) | ((r >> 2) & 3);
+    return (line << 7) + (((c & 15) ^ s) << 3);
+  } else if constexpr (CPR == 8) {
+    const int line = r >> 1;
+    const int s = ((line & 1) << 2) | ((line >> 1) & 3);
+    return (line << 7) + (((((r & 1) << 3) | c) ^ s) << 3);
+  } else {
+    static_assert(CPR == 4, "head dim must be 32, 64, 128 or 256");
+    const int line = r >> 2;
+    return (line << 7) + (((((r & 3) << 2) | c) ^ (line & 3)) << 3);
+  }
+}
+
+// A operand of a 32x32x16 product read transposed from a swizzled tile: the
+// lane gets column (col0 + lane % 32) of rows 16cc + {4g .. 4g+3, 8+4g .. 8+4g+3}
+// (g = lane / 32), the key order of the score accumulators.
+template <int D>
+__device__ inline u32x4 tr_operand(const uint16_t* tile, int lane, int cc, int col0) {
+  const int g = lane >> 5, j = lane & 15;
+  const int r = 16 * cc + 4 * g + (j >> 2);
+  const int d = col0 + 16 * ((lane & 31) >> 4) + 4 * (j & 3);
+  const u32x2 lo = lds_read_tr16(tile + swz_off<D>(r, d >> 3) + (d & 7));
+  const u32x2 hi = lds_read_tr16(tile + swz_off<D>(r + 8, d >> 3) + (d & 7));
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// Per-score transform shared by both kernels: the recomputed probability and
+// the softcap derivative.  `lse2` is the row's LSE in log2 units (+inf for
+// rows that see no key or lie past the sequence, giving P = 0).
+template <bool GENERIC>
+__device__ inline float bwd_prob(const BwdParams& p, float s, float lse2, float slope, int qpos,
+                                 int key, float& cap_grad) {
+  cap_grad = 1.f;
+  if (!GENERIC) return __builtin_amdgcn_exp2f(fmaf(s, p.scale_log2, -lse2));
+  float x = s * p.scale;
+  if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qpos - key)), x);
+  if (p.softcap > 0.f) {
+    // tanh(x / softcap) = 1 - 2 / (1 + e^(2x/softcap))
+    const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
+    const float th = 1.f - 2.f * __builtin_amdgcn_rcpf(1.f + e2);
+    x = p.softcap * th;
+    cap_grad = 1.f - th * th;
+  }
+  return __builtin_amdgcn_exp2f(fmaf(x, kLog2e, -lse2));
+}
+
+// Row base offsets of one (batch, head) for the dense or varlen layout.
+__device__ inline int64_t row_base(const BwdParams& p, int64_t sb, int64_t ss, int64_t sh, int b,
+                                   int head, int start) {
+  return (p.cu_q != nullptr ? (int64_t)start * ss : (int64_t)b * sb) + (int64_t)head * sh;
+}
+
+template <class T, int D, int NW, int BN>
+struct BwdDqTile {
+  static constexpr int BM = 32 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int TILE = BN * D;                    // elements per K or V tile
+  static constexpr int LDS_BYTES = 2 * 2 * TILE * 2;     // K, V x 2 slots
+};
+
+template <class T, int D, int NW, int BN, bool GENERIC, int WPE>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void bwd_dq_kernel(const BwdParams p) {
+  using Tile = BwdDqTile<T, D, NW, BN>;
+  constexpr int BM = Tile::BM, NT = Tile::NT, TILE = Tile::TILE;
+  constexpr int CPR = D / 8;
+  constexpr int CHUNKS = BN * CPR;
+  constexpr int KPT = (CHUNKS + NT - 1) / NT;
+  constexpr int NKC = D / 16, NDB = D / 32, NKB = BN / 32, NCC = BN / 16;
+  static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31;
+  const int g = lane >> 5;
+
+  // ------------------------------------------------------------ work item
+  int id = xcd_remap(blockIdx.x, p.total_blocks);
+  const int mb = p.n_blocks - 1 - id % p.n_blocks;   // late (longer) rows first
+  id /= p.n_blocks;
+  const int hh = id % p.heads_q;
+  const int b = id / p.heads_q;
+  const int kvh = hh / p.group;
+
+  int Sq = p.seqlen_q, Sk = p.seqlen_k, qs = 0, ks = 0;
+  if (p.cu_q != nullptr) {
+    qs = p.cu_q[b];
+    ks = p.cu_k[b];
+    Sq = p.cu_q[b + 1] - qs;
+    Sk = p.cu_k[b + 1] - ks;
+  }
+  const int row0 = mb * BM;
+  if (row0 >= Sq) return;
+  const int row_last = min(row0 + BM, Sq) - 1;
+  const int qi = row0 + w * 32 + c32;
+  const bool row_valid = qi < Sq;
+  const int qoff = (int)p.q_offset;
+  const int qpos = qi + qoff;
+
+  const int64_t lse_base = row_base(p, p.lse_sb, p.lse_ss, p.lse_sh, b, hh, qs);
+  float slope = 0.f;
+  if (GENERIC && p.alibi != nullptr) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
+
+  const int wrow0 = row0 + w * 32;
+  const bool wave_active = wrow0 <= row_last;
+  const int qpos_w_min = wrow0 + qoff;
+  const int qpos_w_max = min(wrow0 + 31, row_last) + qoff;
+  const int wl = p.window_left, wr = p.window_right;
+  const bool causal = p.causal != 0;
+  int key_hi = Sk - 1;
+  if (causal) key_hi = min(key_hi, qpos);
+  if (wr >= 0) key_hi = min(key_hi, qpos + wr);
+  const int key_lo = wl >= 0 ? qpos - wl : -(1 << 30);
+
+  int k_hi = Sk;
+  if (causal) k_hi = min(k_hi, row_last + qoff + 1);
+  if (wr >= 0) k_hi = min(k_hi, row_last + qoff + wr + 1);
+  int k_lo = 0;
+  if (wl >= 0) k_lo = max(0, row0 + qoff - wl);
+  const int t_begin = k_lo / BN;
+  const int t_end = k_hi > k_lo ? (k_hi + BN - 1) / BN : t_begin;
+
+  // ------------------------------------------------------------ Q, dO rows; delta
+  u32x4 qreg[NKC], doreg[NKC];
+  float dsum = 0.f;
+  {
+    const uint16_t* qrow = static_cast<const uint16_t*>(p.q) +
+                           row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hh, qs) + (int64_t)qi * p.q_ss;
+    const uint16_t* drow = static_cast<const uint16_t*>(p.dout) +
+                           row_base(p, p.do_sb, p.do_ss, p.do_sh, b, hh, qs) + (int64_t)qi * p.do_ss;
+    const uint16_t* orow = static_cast<const uint16_t*>(p.o) +
+                           row_base(p, p.o_sb, p.o_ss, p.o_sh, b, hh, qs) + (int64_t)qi * p.o_ss;
+#pragma unroll
+    for (int kc = 0; kc < NKC; ++kc) {
+      const int d = kc * 16 + g * 8;
+      const u32x4 z = {0, 0, 0, 0};
+      qreg[kc] = row_valid ? load16(qrow + d) : z;
+      doreg[kc] = row_valid ? load16(drow + d) : z;
+      const u32x4 o4 = row_valid ? load16(orow + d) : z;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        dsum = fmaf(T::to_float((uint16_t)(o4[e] & 0xffffu)),
+                    T::to_float((uint16_t)(doreg[kc][e] & 0xffffu)), dsum);
+        dsum = fmaf(T::to_float((uint16_t)(o4[e] >> 16)), T::to_float((uint16_t)(doreg[kc][e] >> 16)),
+                    dsum);
+      }
+    }
+  }
+  const float delta = halves_sum(dsum);
+  float lse2 = INFINITY;
+  if (row_valid) {
+    const float l = p.lse[lse_base + (int64_t)qi * p.lse_ss];
+    if (l != -INFINITY) lse2 = l * kLog2e;
+    if (g == 0) p.delta[lse_base + (int64_t)qi * p.lse_ss] = delta;
+  }
+
+  // ------------------------------------------------------------ K / V tiles
+  const uint16_t* kg = static_cast<const uint16_t*>(p.k) + row_base(p, p.k_sb, p.k_ss, p.k_sh, b, kvh, ks);
+  const uint16_t* vg = static_cast<const uint16_t*>(p.v) + row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks);
+  const uint32_t k_row_b = (uint32_t)(p.k_ss * 2);
+  const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
+  uint32_t k_off[KPT], v_off[KPT];
+  int l_off[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int c = tid + i * NT;
+    k_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * k_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
+    v_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
+    l_off[i] = swz_off<D>(c / CPR, c % CPR);
+  }
+  u32x4 kreg[KPT], vreg[KPT];
+  auto load_tiles = [&](int t) {
+    const int n0 = t * BN;
+    const auto rk = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
+    const auto rv = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      kreg[i] = buf_load16(rk, k_off[i], 0);
+      vreg[i] = buf_load16(rv, v_off[i], 0);
+    }
+  };
+  auto k_slot = [&](int i) { return smem + (i & 1) * TILE; };
+  auto v_slot = [&](int i) { return smem + 2 * TILE + (i & 1) * TILE; };
+  auto store_tiles = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int c = tid + i * NT;
+      if (CHUNKS % NT == 0 || c < CHUNKS) {
+        store16(k_slot(slot) + l_off[i], kreg[i]);
+        store16(v_slot(slot) + l_off[i], vreg[i]);
+      }
+    }
+  };
+
+  auto wave_skips = [&](int t) {
+    const int n0 = t * BN, n1 = n0 + BN;
+    bool skip = !wave_active || n0 >= Sk;
+    if (causal) skip = skip || n0 > qpos_w_max;
+    if (wr >= 0) skip = skip || n0 > qpos_w_max + wr;
+    if (wl >= 0) skip = skip || n1 - 1 < qpos_w_min - wl;
+    return skip;
+  };
+  auto wave_masks = [&](int t) {
+    const int n0 = t * BN, n1 = n0 + BN;
+    bool need = n1 > Sk;
+    if (causal) need = need || n1 - 1 > qpos_w_min;
+    if (wr >= 0) need = need || n1 - 1 > qpos_w_min + wr;
+    if (wl >= 0) need = need || n0 < qpos_w_max - wl;
+    return need;
+  };
+
+  f32x16 acc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+
+  auto tile_math = [&](int t, int slot, bool masked) {
+    const uint16_t* Ks = k_slot(slot);
+    const uint16_t* Vs = v_slot(slot);
+    f32x16 s[NKB], dp[NKB];
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      s[kb] = f32x16{};
+      dp[kb] = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        const int off = swz_off<D>(kb * 32 + c32, 2 * kc + g);
+        s[kb] = T::mfma32(load16(Ks + off), qreg[kc], s[kb]);
+        dp[kb] = T::mfma32(load16(Vs + off), doreg[kc], dp[kb]);
+      }
+    }
+    const int n0 = t * BN;
+    u32x4 dsb[NCC];
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+      const int kb = cc >> 1, o8 = (cc & 1) * 8;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float ds[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int v = o8 + 2 * j + u;
+          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+          float cg;
+          float pr = bwd_prob<GENERIC>(p, s[kb][v], lse2, slope, qpos, key, cg);
+          if (masked && (key < key_lo || key > key_hi)) pr = 0.f;
+          ds[u] = pr * (dp[kb][v] - delta) * cg;
+        }
+        dsb[cc][j] = T::pack2(ds[0], ds[1]);
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+        acc[db] = T::mfma32(tr_operand<D>(Ks, lane, cc, db * 32), dsb[cc], acc[db]);
+    }
+  };
+
+  // ------------------------------------------------------------ main loop
+  const int J = t_end - t_begin;
+  if (J > 0) {
+    load_tiles(t_begin);
+    store_tiles(0);
+  }
+  for (int it = 0; it < J; ++it) {
+    const int t = t_begin + it;
+    __syncthreads();
+    const bool has_next = it + 1 < J;
+    if (has_next) load_tiles(t + 1);
+    if (!wave_skips(t)) tile_math(t, it, wave_masks(t));
+    if (has_next) store_tiles(it + 1);
+  }
+
+  // ------------------------------------------------------------ dQ = scale * acc
+  if (!row_valid) return;
+  uint16_t* dqrow = static_cast<uint16_t*>(p.dq) + row_base(p, p.dq_sb, p.dq_ss, p.dq_sh, b, hh, qs) +
+                    (int64_t)qi * p.dq_ss;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = db * 32 + r * 8 + g * 4;
+      u32x2 val;
+      val[0] = T::pack2(acc[db][4 * r] * p.scale, acc[db][4 * r + 1] * p.scale);
+      val[1] = T::pack2(acc[db][4 * r + 2] * p.scale, acc[db][4 * r + 3] * p.scale);
+      *reinterpret_cast<u32x2*>(dqrow + d) = val;
+    }
+  }
+}
+
+template <class T, int D, int NW, int BM>
+struct BwdDkvTile {
+  static constexpr int BN = 32 * NW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int TILE = BM * D;                           // elements per Q or dO tile
+  static constexpr int LDS_BYTES = 2 * 2 * TILE * 2 + 2 * 2 * BM * 4;   // + lse2, delta
+};
+
+// PASS 0 accumulates dK and dV together; at D = 256 the two accumulators do
+// not fit beside K and V, so the launcher runs PASS 1 (dV only) and PASS 2 (dK
+// only), recomputing S in each.
+template <class T, int D, int NW, int BM, bool GENERIC, int WPE, int PASS>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void bwd_dkdv_kernel(const BwdParams p) {
+  constexpr bool DO_DV = PASS != 2, DO_DK = PASS != 1;
+  using Tile = BwdDkvTile<T, D, NW, BM>;
+  constexpr int BN = Tile::BN, NT = Tile::NT, TILE = Tile::TILE;
+  constexpr int CPR = D / 8;
+  constexpr int CHUNKS = BM * CPR;
+  constexpr int KPT = (CHUNKS + NT - 1) / NT;
+  constexpr int NKC = D / 16, NDB = D / 32, NRB = BM / 32, NCC = BM / 16;
+  static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
+  static_assert(BM <= NT, "one thread per row stages LSE and delta");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  float* fsm = reinterpret_cast<float*>(smem + 4 * TILE);   // [lse2 x2][delta x2]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c32 = lane & 31;
+  const int g = lane >> 5;
+
+  // ------------------------------------------------------------ work item
+  int id = xcd_remap(blockIdx.x, p.total_blocks);
+  const int nb = id % p.n_blocks;
+  id /= p.n_blocks;
+  const int kvh = id % p.heads_k;
+  const int b = id / p.heads_k;
+
+  int Sq = p.seqlen_q, Sk = p.seqlen_k, qs = 0, ks = 0;
+  if (p.cu_q != nullptr) {
+    qs = p.cu_q[b];
+    ks = p.cu_k[b];
+    Sq = p.cu_q[b + 1] - qs;
+    Sk = p.cu_k[b + 1] - ks;
+  }
+  const int key0 = nb * BN;
+  if (key0 >= Sk) return;
+  const int key_last = min(key0 + BN, Sk) - 1;
+  const int kj = key0 + w * 32 + c32;
+  const bool key_valid = kj < Sk;
+  const int qoff = (int)p.q_offset;
+  const int wl = p.window_left, wr = p.window_right;
+  const bool causal = p.causal != 0;
+
+  // K and V rows of this lane's key: B operands of S = Q K^T and dP = dO V^T.
+  u32x4 kreg[NKC], vreg[NKC];
+  {
+    const uint16_t* krow = static_cast<const uint16_t*>(p.k) +
+                           row_base(p, p.k_sb, p.k_ss, p.k_sh, b, kvh, ks) + (int64_t)kj * p.k_ss;
+    const uint16_t* vrow = static_cast<const uint16_t*>(p.v) +
+                           row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks) + (int64_t)kj * p.v_ss;
+#pragma unroll
+    for (int kc = 0; kc < NKC; ++kc) {
+      const u32x4 z = {0, 0, 0, 0};
+      kreg[kc] = key_valid ? load16(krow + kc * 16 + g * 8) : z;
+      vreg[kc] = key_valid && DO_DK ? load16(vrow + kc * 16 + g * 8) : z;
+    }
+  }
+
+  // Query rows i that see a key of this block: [q_lo, q_hi).
+  int q_lo = 0, q_hi = Sq;
+  if (causal) q_lo = max(q_lo, key0 - qoff);
+  if (wr >= 0) q_lo = max(q_lo, key0 - qoff - wr);
+  if (wl >= 0) q_hi = min(q_hi, key_last - qoff + wl + 1);
+  const int m_begin = q_lo / BM;
+  const int m_end = q_hi > q_lo ? (q_hi + BM - 1) / BM : m_begin;
+  const int NM = m_end - m_begin;
+  const int J = NM * p.group;
+
+  // This wave's keys [wk0, wk1] and the tiles it may skip or must mask.
+  const int wk0 = key0 + w * 32;
+  const int wk1 = min(wk0 + 31, Sk - 1);
+  const bool wave_active = wk0 < Sk;
+  auto wave_skips = [&](int m0) {
+    const int p0 = m0 + qoff, p1 = m0 + BM - 1 + qoff;
+    bool skip = !wave_active;
+    if (causal) skip = skip || p1 < wk0;
+    if (wr >= 0) skip = skip || p1 + wr < wk0;
+    if (wl >= 0) skip = skip || p0 - wl > wk1;
+    return skip;
+  };
+  auto wave_masks = [&](int m0) {
+    const int p0 = m0 + qoff, p1 = m0 + BM - 1 + qoff;
+    bool need = false;
+    if (causal) need = need || p0 < wk1;
+    if (wr >= 0) need = need || p0 + wr < wk1;
+    if (wl >= 0) need = need || p1 - wl > wk0;
+    return need;
+  };
+
+  // ------------------------------------------------------------ Q / dO tiles
+  const uint16_t* qg0 = static_cast<const uint16_t*>(p.q);
+  const uint16_t* dg0 = static_cast<const uint16_t*>(p.dout);
+  const uint32_t q_row_b = (uint32_t)(p.q_ss * 2);
+  const uint32_t d_row_b = (uint32_t)(p.do_ss * 2);
+  uint32_t q_off[KPT], d_off[KPT];
+  int l_off[KPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int c = tid + i * NT;
+    q_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * q_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
+    d_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * d_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
+    l_off[i] = swz_off<D>(c / CPR, c % CPR);
+  }
+  u32x4 qst[KPT], dst[KPT];
+  float lse_st = INFINITY, delta_st = 0.f;
+  auto head_of = [&](int it) { return kvh * p.group + it / NM; };
+  auto m0_of = [&](int it) { return (m_begin + it % NM) * BM; };
+  auto load_tiles = [&](int it) {
+    const int hq = head_of(it), m0 = m0_of(it);
+    const uint16_t* qg = qg0 + row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hq, qs) + (int64_t)m0 * p.q_ss;
+    const uint16_t* dg = dg0 + row_base(p, p.do_sb, p.do_ss, p.do_sh, b, hq, qs) + (int64_t)m0 * p.do_ss;
+    const auto rq = make_rsrc(qg, rows_extent(m0, Sq, p.q_ss, D));
+    const auto rd = make_rsrc(dg, rows_extent(m0, Sq, p.do_ss, D));
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      qst[i] = buf_load16(rq, q_off[i], 0);
+      dst[i] = buf_load16(rd, d_off[i], 0);
+    }
+    lse_st = INFINITY;
+    delta_st = 0.f;
+    if (tid < BM && m0 + tid < Sq) {
+      const int64_t li = row_base(p, p.lse_sb, p.lse_ss, p.lse_sh, b, hq, qs) + (int64_t)(m0 + tid) * p.lse_ss;
+      const float l = p.lse[li];
+      if (l != -INFINITY) lse_st = l * kLog2e;
+      delta_st = p.delta[li];
+    }
+  };
+  auto q_slot = [&](int i) { return smem + (i & 1) * TILE; };
+  auto d_slot = [&](int i) { return smem + 2 * TILE + (i & 1) * TILE; };
+  auto store_tiles = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i) {
+      const int c = tid + i * NT;
+      if (CHUNKS % NT == 0 || c < CHUNKS) {
+        store16(q_slot(slot) + l_off[i], qst[i]);
+        store16(d_slot(slot) + l_off[i], dst[i]);
+      }
+    }
+    if (tid < BM) {
+      fsm[(slot & 1) * BM + tid] = lse_st;
+      fsm[2 * BM + (slot & 1) * BM + tid] = delta_st;
+    }
+  };
+
+  f32x16 dk[NDB], dv[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+    dk[db] = f32x16{};
+    dv[db] = f32x16{};
+  }
+
+  auto tile_math = [&](int it, int slot, bool masked) {
+    const uint16_t* Qs = q_slot(slot);
+    const uint16_t* Ds = d_slot(slot);
+    const float* Ls = fsm + (slot & 1) * BM;
+    const float* Es = fsm + 2 * BM + (slot & 1) * BM;
+    const int hq = head_of(it), m0 = m0_of(it);
+    float slope = 0.f;
+    if (GENERIC && p.alibi != nullptr) slope = p.alibi[(int64_t)b * p.alibi_sb + hq];
+    f32x16 s[NRB], dp[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      s[rb] = f32x16{};
+      dp[rb] = f32x16{};
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
+        s[rb] = T::mfma32(load16(Qs + off), kreg[kc], s[rb]);
+        if (DO_DK) dp[rb] = T::mfma32(load16(Ds + off), vreg[kc], dp[rb]);
+      }
+    }
+    u32x4 pb[NCC], dsb[NCC];
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+      const int rb = cc >> 1, o8 = (cc & 1) * 8;
+      // Slots o8 .. o8+7 hold rows 16cc + 4g + {0..3} and 16cc + 8 + 4g + {0..3}.
+      const int r0 = 16 * cc + 4 * g;
+      const f32x4 l0 = *reinterpret_cast<const f32x4*>(Ls + r0);
+      const f32x4 l1 = *reinterpret_cast<const f32x4*>(Ls + r0 + 8);
+      const f32x4 e0 = *reinterpret_cast<const f32x4*>(Es + r0);
+      const f32x4 e1 = *reinterpret_cast<const f32x4*>(Es + r0 + 8);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float pv[2], ds[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int v = o8 + 2 * j + u;          // accumulator slot
+          const int rr = 2 * j + u;              // 0..7: rows r0 + rr%4 (+8 for rr >= 4)
+          const float lse2 = rr < 4 ? l0[rr] : l1[rr - 4];
+          const float dl = rr < 4 ? e0[rr] : e1[rr - 4];
+          const int row = m0 + r0 + (rr & 3) + (rr >= 4 ? 8 : 0);
+          const int qpos = row + qoff;
+          float cg;
+          float pr = bwd_prob<GENERIC>(p, s[rb][v], lse2, slope, qpos, kj, cg);
+          if (masked) {
+            bool vis = true;
+            if (causal) vis = vis && kj <= qpos;
+            if (wr >= 0) vis = vis && kj <= qpos + wr;
+            if (wl >= 0) vis = vis && kj >= qpos - wl;
+            if (!vis) pr = 0.f;
+          }
+          pv[u] = pr;
+          ds[u] = pr * (dp[rb][v] - dl) * cg;
+        }
+        pb[cc][j] = T::pack2(pv[0], pv[1]);
+        dsb[cc][j] = T::pack2(ds[0], ds[1]);
+      }
+    }
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc) {
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        if (DO_DV) dv[db] = T::mfma32(tr_operand<D>(Ds, lane, cc, db * 32), pb[cc], dv[db]);
+        if (DO_DK) dk[db] = T::mfma32(tr_operand<D>(Qs, lane, cc, db * 32), dsb[cc], dk[db]);
+      }
+    }
+  };
+
+  // ------------------------------------------------------------ main loop
+  if (J > 0) {
+    load_tiles(0);
+    store_tiles(0);
+  }
+  for (int it = 0; it < J; ++it) {
+    __syncthreads();
+    const bool has_next = it + 1 < J;
+    if (has_next) load_tiles(it + 1);
+    const int m0 = m0_of(it);
+    if (!wave_skips(m0)) tile_math(it, it, wave_masks(m0));
+    if (has_next) store_tiles(it + 1);
+  }
+
+  // ------------------------------------------------------------ dK = scale * dK^T, dV
+  if (!key_valid) return;
+  uint16_t* dkrow = static_cast<uint16_t*>(p.dk) + row_base(p, p.dk_sb, p.dk_ss, p.dk_sh, b, kvh, ks) +
+                    (int64_t)kj * p.dk_ss;
+  uint16_t* dvrow = static_cast<uint16_t*>(p.dv) + row_base(p, p.dv_sb, p.dv_ss, p.dv_sh, b, kvh, ks) +
+                    (int64_t)kj * p.dv_ss;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = db * 32 + r * 8 + g * 4;
+      u32x2 vk, vv;
+      vk[0] = T::pack2(dk[db][4 * r] * p.scale, dk[db][4 * r + 1] * p.scale);
+      vk[1] = T::pack2(dk[db][4 * r + 2] * p.scale, dk[db][4 * r + 3] * p.scale);
+      vv[0] = T::pack2(dv[db][4 * r], dv[db][4 * r + 1]);
+      vv[1] = T::pack2(dv[db][4 * r + 2], dv[db][4 * r + 3]);
+      if (DO_DK) *reinterpret_cast<u32x2*>(dkrow + d) = vk;
+      if (DO_DV) *reinterpret_cast<u32x2*>(dvrow + d) = vv;
+    }
+  }
+}
+
+}  // namespace fa

@@ -1,0 +1,90 @@
+// Host-side launch helpers for the backward kernels (fa_bwd_kernel.h): tile
+// choice per head dim and the grids.  Instantiated once per element type
+// (fa_bwd_f16.hip, fa_bwd_bf16.hip).
+#pragma once
+
+#include "fa_bwd_kernel.h"
+
+namespace fa {
+
+// dQ: 4 waves x 32 query rows, 64-key tiles (32 from D = 128, where Q, dO and
+// the dQ^T accumulators take 128 registers; 256 at D = 256).  dK/dV: 4 waves
+// x 32 keys, 64 query rows per tile (32 from D = 128); the dK^T / dV^T
+// accumulators live in the accumulation registers, one wave per SIMD; D = 256
+// accumulates dV and dK in two passes.
+template <int D> struct BwdCfg {
+  static constexpr int DQ_NW = 4, DQ_BN = D >= 128 ? 32 : 64, DQ_WPE = D >= 256 ? 1 : 2;
+  static constexpr int KV_NW = 4, KV_BM = D >= 128 ? 32 : 64, KV_WPE = 1;
+};
+
+template <class Kern>
+hipError_t set_lds(Kern kern, int bytes, bool& done) {
+  if (done) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess) done = true;
+  return e;
+}
+
+template <class T, int D, bool GEN, int PASS>
+hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
+  using C = BwdCfg<D>;
+  using Tile = BwdDkvTile<T, D, C::KV_NW, C::KV_BM>;
+  auto kern = bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, GEN, C::KV_WPE, PASS>;
+  static bool lds_set = false;
+  hipError_t e = set_lds(kern, Tile::LDS_BYTES, lds_set);
+  if (e != hipSuccess) return e;
+  p.n_blocks = (p.seqlen_k + Tile::BN - 1) / Tile::BN;
+  const int64_t total = (int64_t)p.n_blocks * p.heads_k * p.batch;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (total <= 0) return hipSuccess;
+  p.total_blocks = (int)total;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  return hipGetLastError();
+}
+
+template <class T, int D, bool GEN>
+hipError_t launch_bwd_d(BwdParams p, hipStream_t st) {
+  using C = BwdCfg<D>;
+  {
+    using Tile = BwdDqTile<T, D, C::DQ_NW, C::DQ_BN>;
+    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, GEN, C::DQ_WPE>;
+    static bool lds_set = false;
+    hipError_t e = set_lds(kern, Tile::LDS_BYTES, lds_set);
+    if (e != hipSuccess) return e;
+    p.n_blocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
+    const int64_t total = (int64_t)p.n_blocks * p.heads_q * p.batch;
+    if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+    if (total > 0) {
+      p.total_blocks = (int)total;
+      hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
+  }
+  if constexpr (D >= 256) {
+    hipError_t e = launch_dkdv<T, D, GEN, 1>(p, st);
+    if (e != hipSuccess) return e;
+    return launch_dkdv<T, D, GEN, 2>(p, st);
+  } else {
+    return launch_dkdv<T, D, GEN, 0>(p, st);
+  }
+}
+
+template <class T>
+hipError_t launch_bwd(const BwdParams& p, int head_dim, bool generic, hipStream_t st) {
+#define FA_CASE(DD)                                                              \
+  case DD:                                                                       \
+    return generic ? launch_bwd_d<T, DD, true>(p, st) : launch_bwd_d<T, DD, false>(p, st);
+  switch (head_dim) {
+    FA_CASE(32)
+    FA_CASE(64)
+    FA_CASE(128)
+    FA_CASE(256)
+    default:
+      return hipErrorInvalidValue;
+  }
+#undef FA_CASE
+}
+
+}  // namespace fa

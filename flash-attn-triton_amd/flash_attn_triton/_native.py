@@ -47,6 +47,10 @@ _SIGNATURES = {
     "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
                              _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+    "fa_bwd_dense": (_int, [_vp] * 10 + [_i64] * 6 + [_i64p] * 9 +
+                     [_int, _f32, _int, _i64, _i64, _i64, _f32, _vp, _i64, _vp]),
+    "fa_bwd_varlen": (_int, [_vp] * 12 + [_i64] * 6 + [_i64p] * 9 +
+                      [_int, _f32, _int, _i64, _i64, _f32, _vp, _i64, _vp]),
     "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
     "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
@@ -139,6 +143,43 @@ def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offse
         _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)), _ptr(bias), bias_stride,
         _stream(q.device))
     _check(status, "fa_fwd_dense")
+
+
+def bwd_dense(q, k, v, out, dout, lse, dq, dk, dv, delta, softmax_scale: float, causal: bool,
+              q_pos_offset: int, window_left: int, window_right: int, softcap: float,
+              alibi) -> None:
+    """Gradients of fwd_dense: all tensors BSHD ([B,S,H,D]); lse / delta fp32
+    [B,Hq,Sq]; dq/dk/dv are written.  See fa_bwd_dense."""
+    lib = load()
+    B, Sq, Hq, D = q.shape
+    Sk, Hk = k.shape[1], k.shape[2]
+    st = [_strides(t.stride()[:3]) for t in (q, k, v, out, dout, dq, dk, dv)]
+    status = lib.fa_bwd_dense(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq), _ptr(dk),
+        _ptr(dv), _ptr(delta), B, Sq, Sk, Hq, Hk, D, *st, _strides(lse.stride()),
+        dtype_code(q.dtype), float(softmax_scale), int(bool(causal)), int(q_pos_offset),
+        int(window_left), int(window_right), float(softcap), _ptr(alibi),
+        0 if alibi is None else int(alibi.stride(0)), _stream(q.device))
+    _check(status, "fa_bwd_dense")
+
+
+def bwd_varlen(q, k, v, out, dout, lse, dq, dk, dv, delta, cu_q, cu_k, max_seqlen_q: int,
+               max_seqlen_k: int, softmax_scale: float, causal: bool, window_left: int,
+               window_right: int, softcap: float, alibi) -> None:
+    """Gradients of fwd_varlen: packed [T,H,D] tensors, lse / delta fp32 [Tq,Hq],
+    cu_* int32 [batch+1].  See fa_bwd_varlen."""
+    lib = load()
+    Hq, D = q.shape[1], q.shape[2]
+    Hk = k.shape[1]
+    st = [_strides(t.stride()[:2]) for t in (q, k, v, out, dout, dq, dk, dv)]
+    status = lib.fa_bwd_varlen(
+        _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq), _ptr(dk),
+        _ptr(dv), _ptr(delta), _ptr(cu_q), _ptr(cu_k), cu_q.numel() - 1, int(max_seqlen_q),
+        int(max_seqlen_k), Hq, Hk, D, *st, _strides(lse.stride()), dtype_code(q.dtype),
+        float(softmax_scale), int(bool(causal)), int(window_left), int(window_right),
+        float(softcap), _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)),
+        _stream(q.device))
+    _check(status, "fa_bwd_varlen")
 
 
 def attn_probs(q, k, lse, probs, lse_out, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,

@@ -18,8 +18,11 @@ defect or a host-side copy, never changes a correct result):
   Python loop of gathers and O(L^2) padded launches, and its causal
   alignment is bottom-right for every cache length (the reference's dense
   stage split drops keys past the first tile when ``L > BLOCK_M``);
-* only the forward pass exists: ``backward`` raises ``NotImplementedError``,
-  and ``dropout_p > 0`` is rejected.
+* gradients run on HIP backward kernels for fp16 / bf16 dense, cross and
+  varlen calls (deterministic: grouped KV heads are reduced in the kernel,
+  not with atomics); fp32 inputs, ``attn_bias``, seqused / paged varlen and
+  the KV-cache path are forward only (``backward`` raises
+  ``NotImplementedError``), and ``dropout_p > 0`` is rejected.
 """
 from __future__ import annotations
 
@@ -35,7 +38,9 @@ from .triton_kernel.attention_kernel import (
     _wrap_grad,
     attention,
     attention_varlen,
+    dense_attention,
     dense_forward,
+    varlen_attention,
     varlen_forward,
 )
 from . import _native
@@ -102,7 +107,7 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     alibi = None
     if alibi_slopes is not None:
         alibi = _normalize_alibi(alibi_slopes, batch, q_heads, q.device)
-    out, lse = dense_forward(q, k, v, softmax_scale=scale, causal=causal,
+    out, lse = dense_attention(q, k, v, softmax_scale=scale, causal=causal,
                              q_pos_offset=causal_offset, window_left=window_size[0],
                              window_right=window_size[1], softcap=softcap, alibi=alibi,
                              return_lse=True, bias=bias)
@@ -110,7 +115,7 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse, probs, None, None, None,
                        q_len, k_len, scale, causal, causal_offset, window_size[0],
                        window_size[1], softcap, alibi, bias)
-    return _wrap_grad(out, q, k, v), lse, probs
+    return out, lse, probs
 
 
 def _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
@@ -126,7 +131,7 @@ def _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen
         raise NotImplementedError(DROPOUT_MSG)
     batch = cu_seqlens_q.numel() - 1
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else softmax_scale
-    out, lse_tok = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+    out, lse_tok = varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                   max_seqlen_k, softmax_scale=scale, causal=causal,
                                   window_left=window_size[0], window_right=window_size[1],
                                   softcap=softcap, alibi=alibi, return_lse=True)
@@ -136,7 +141,7 @@ def _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen
     _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse_tok, probs, lses, cu_seqlens_q,
                        cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal, 0,
                        window_size[0], window_size[1], softcap, alibi)
-    return _wrap_grad(out, q, k, v), lses, probs
+    return out, lses, probs
 
 
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -215,10 +220,9 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
         raise NotImplementedError(DROPOUT_MSG)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(head_dim)
-    out = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
-                        window_left=window_size[0], window_right=window_size[1],
-                        softcap=softcap, alibi=alibi_slopes if use_alibi else None)
-    return _wrap_grad(out, q, k, v)
+    return dense_attention(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                           window_left=window_size[0], window_right=window_size[1],
+                           softcap=softcap, alibi=alibi_slopes if use_alibi else None)
 
 
 def flash_attn_func_cross(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -270,11 +274,10 @@ def flash_attn_func_cross(q, k, v, dropout_p=0.0, softmax_scale=None, causal=Fal
         raise NotImplementedError(DROPOUT_MSG)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
-    out = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
-                        q_pos_offset=_causal_offset, window_left=window_size[0],
-                        window_right=window_size[1], softcap=softcap,
-                        alibi=alibi_slopes if use_alibi else None)
-    return _wrap_grad(out, q, k, v)
+    return dense_attention(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                           q_pos_offset=_causal_offset, window_left=window_size[0],
+                           window_right=window_size[1], softcap=softcap,
+                           alibi=alibi_slopes if use_alibi else None)
 
 
 def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -671,14 +674,20 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     if seqused_q is not None:
         cu_out = torch.zeros((batch_size + 1,), dtype=torch.int32, device=q.device)
         torch.cumsum(seqused_q, 0, out=cu_out[1:])
-    out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                         softmax_scale=softmax_scale, causal=causal,
-                         window_left=window_size[0], window_right=window_size[1],
-                         softcap=softcap, alibi=alibi if use_alibi else None,
-                         seqused_q=seqused_q, seqused_k=seqused_k,
-                         out_rows=values[out_rows] if out_rows is not None else None,
-                         cu_out=cu_out, block_table=block_table)
-    return _wrap_grad(out, q, k, v)
+    if paged or seqused_q is not None or seqused_k is not None:
+        # Forward only: gradients through the block table and used counts are not built.
+        out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                             softmax_scale=softmax_scale, causal=causal,
+                             window_left=window_size[0], window_right=window_size[1],
+                             softcap=softcap, alibi=alibi if use_alibi else None,
+                             seqused_q=seqused_q, seqused_k=seqused_k,
+                             out_rows=values[out_rows] if out_rows is not None else None,
+                             cu_out=cu_out, block_table=block_table)
+        return _wrap_grad(out, q, k, v)
+    return varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                            softmax_scale=softmax_scale, causal=causal,
+                            window_left=window_size[0], window_right=window_size[1],
+                            softcap=softcap, alibi=alibi if use_alibi else None)
 
 
 def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,

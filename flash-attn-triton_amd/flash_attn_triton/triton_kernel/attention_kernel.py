@@ -1,4 +1,4 @@
-"""Low-level forward launch layer (no Triton inside: the module path is kept for drop-in imports).
+"""Low-level launch layer (no Triton inside: the module path is kept for drop-in imports).
 
 Mirrors the public launch functions of the reference's
 ``flash_attn_triton/triton_kernel/attention_kernel.py``:
@@ -10,9 +10,12 @@ Both call the gfx950 HIP kernels of ``libfa_gfx950.so`` through ``_native``.
 The kernels handle ragged lengths, strided inputs and grouped KV heads
 directly, so nothing is padded, repeated or copied on the host.
 
-Only the forward pass exists.  Calling ``backward`` through these functions
-raises ``NotImplementedError``; dropout is not built either and is rejected
-before launch.
+Autograd: when q, k or v requires grad the forward also keeps the LSE and the
+backward runs ``fa_bwd_dense`` / ``fa_bwd_varlen`` (the reference's
+``_attention.backward`` :1185-1198 and ``_attention_varlen.backward``
+:1322-1361), fp16 and bf16.  Not differentiable (backward raises
+``NotImplementedError``): fp32 inputs, ``attn_bias``, seqused / paged varlen
+and the KV-cache path.  Dropout is not built and is rejected before launch.
 """
 from __future__ import annotations
 
@@ -23,18 +26,19 @@ import torch
 
 from .. import _native
 
-__all__ = ["attention", "attention_varlen", "dense_forward", "varlen_forward", "FORWARD_ONLY_MSG"]
+__all__ = ["attention", "attention_varlen", "dense_forward", "varlen_forward", "dense_attention",
+           "varlen_attention", "dense_backward", "varlen_backward", "FORWARD_ONLY_MSG"]
 
 FORWARD_ONLY_MSG = (
-    "flash_attn_triton (gfx950 HIP build): only the forward pass is implemented; "
-    "the backward kernels are not built yet")
+    "flash_attn_triton (gfx950 HIP build): this call has no backward (fp32 inputs, "
+    "attn_bias, seqused / paged varlen and the KV-cache path are forward only)")
 DROPOUT_MSG = (
     "flash_attn_triton (gfx950 HIP build): dropout_p > 0 is not implemented; "
     "call with dropout_p=0.0")
 
 
 class _ForwardOnly(torch.autograd.Function):
-    """Attach a grad_fn that fails loudly: the backward kernels are not built."""
+    """Attach a grad_fn that fails loudly for calls without a backward."""
 
     @staticmethod
     def forward(ctx, out, *inputs):
@@ -117,6 +121,159 @@ def varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
     return (out, lse) if return_lse else out
 
 
+def _needs_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
+def _pad_head_dim(t: torch.Tensor, d: int) -> torch.Tensor:
+    return torch.nn.functional.pad(t, (0, d - t.shape[-1]))
+
+
+def _f32_alibi(alibi, device):
+    return None if alibi is None else alibi.to(device=device, dtype=torch.float32).contiguous()
+
+
+def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: bool,
+                   q_pos_offset: int = 0, window_left: int = -1, window_right: int = -1,
+                   softcap: float = 0.0, alibi: Optional[torch.Tensor] = None):
+    """Gradients ``(dq, dk, dv)`` of ``dense_forward`` from ``dout``, given its
+    output and LSE (``fa_bwd_dense``).  Head dim 16 runs at 32 with zero padding
+    (the extra dims contribute nothing to the scores and get zero gradients)."""
+    if q.dtype == torch.float32:
+        raise NotImplementedError(
+            "flash_attn_triton (gfx950 HIP build): the backward takes fp16 or bf16 inputs; "
+            "fp32 inputs are forward only")
+    if q.shape[-1] == 16:
+        grads = dense_backward(*(_pad_head_dim(t, 32) for t in (q, k, v, out, dout)), lse,
+                               softmax_scale=softmax_scale, causal=causal,
+                               q_pos_offset=q_pos_offset, window_left=window_left,
+                               window_right=window_right, softcap=softcap, alibi=alibi)
+        return tuple(g[..., :16] for g in grads)
+    qk, kk, vk, ok, dok = (_kernel_ready(t) for t in (q, k, v, out, dout))
+    dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.empty(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.empty(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty_like(lse)
+    _native.bwd_dense(qk, kk, vk, ok, dok, lse, dq, dk, dv, delta, softmax_scale, causal,
+                      q_pos_offset, window_left, window_right, softcap,
+                      _f32_alibi(alibi, q.device))
+    return dq, dk, dv
+
+
+def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
+                    *, softmax_scale: float, causal: bool, window_left: int = -1,
+                    window_right: int = -1, softcap: float = 0.0,
+                    alibi: Optional[torch.Tensor] = None):
+    """Gradients ``(dq, dk, dv)`` of ``varlen_forward`` (``fa_bwd_varlen``).
+    Rows outside every sequence get zero gradients."""
+    if q.dtype == torch.float32:
+        raise NotImplementedError(
+            "flash_attn_triton (gfx950 HIP build): the backward takes fp16 or bf16 inputs; "
+            "fp32 inputs are forward only")
+    if q.shape[-1] == 16:
+        grads = varlen_backward(*(_pad_head_dim(t, 32) for t in (q, k, v, out, dout)), lse,
+                                cu_q, cu_k, max_seqlen_q, max_seqlen_k,
+                                softmax_scale=softmax_scale, causal=causal,
+                                window_left=window_left, window_right=window_right,
+                                softcap=softcap, alibi=alibi)
+        return tuple(g[..., :16] for g in grads)
+    qk, kk, vk, ok, dok = (_kernel_ready(t) for t in (q, k, v, out, dout))
+    dq = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
+    dk = torch.zeros(k.shape, dtype=k.dtype, device=k.device)
+    dv = torch.zeros(v.shape, dtype=v.dtype, device=v.device)
+    delta = torch.empty_like(lse)
+    i32 = lambda t: t.to(device=q.device, dtype=torch.int32).contiguous()
+    _native.bwd_varlen(qk, kk, vk, ok, dok, lse, dq, dk, dv, delta, i32(cu_q), i32(cu_k),
+                       max_seqlen_q, max_seqlen_k, softmax_scale, causal, window_left,
+                       window_right, softcap, _f32_alibi(alibi, q.device))
+    return dq, dk, dv
+
+
+class _DenseAttention(torch.autograd.Function):
+    """dense_forward with the fa_bwd_dense backward; returns (out, lse)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, softmax_scale, causal, q_pos_offset, window_left, window_right,
+                softcap, alibi):
+        out, lse = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                                 q_pos_offset=q_pos_offset, window_left=window_left,
+                                 window_right=window_right, softcap=softcap, alibi=alibi,
+                                 return_lse=True)
+        ctx.save_for_backward(q, k, v, out, lse, alibi)
+        ctx.opts = (softmax_scale, causal, q_pos_offset, window_left, window_right, softcap)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse, alibi = ctx.saved_tensors
+        scale, causal, off, wl, wr, cap = ctx.opts
+        dq, dk, dv = dense_backward(q, k, v, out, dout, lse, softmax_scale=scale, causal=causal,
+                                    q_pos_offset=off, window_left=wl, window_right=wr,
+                                    softcap=cap, alibi=alibi)
+        return dq, dk, dv, None, None, None, None, None, None, None
+
+
+class _VarlenAttention(torch.autograd.Function):
+    """varlen_forward with the fa_bwd_varlen backward; returns (out, lse)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
+                window_left, window_right, softcap, alibi):
+        out, lse = varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
+                                  softmax_scale=softmax_scale, causal=causal,
+                                  window_left=window_left, window_right=window_right,
+                                  softcap=softcap, alibi=alibi, return_lse=True)
+        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, alibi)
+        ctx.opts = (max_seqlen_q, max_seqlen_k, softmax_scale, causal, window_left,
+                    window_right, softcap)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, _dlse):
+        q, k, v, out, lse, cu_q, cu_k, alibi = ctx.saved_tensors
+        mq, mk, scale, causal, wl, wr, cap = ctx.opts
+        dq, dk, dv = varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, mq, mk,
+                                     softmax_scale=scale, causal=causal, window_left=wl,
+                                     window_right=wr, softcap=cap, alibi=alibi)
+        return (dq, dk, dv) + (None,) * 10
+
+
+def dense_attention(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: int = 0,
+                    window_left: int = -1, window_right: int = -1, softcap: float = 0.0,
+                    alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
+                    bias: Optional[torch.Tensor] = None):
+    """``dense_forward`` that is differentiable in q, k, v (fp16 / bf16)."""
+    if not _needs_grad(q, k, v) or bias is not None:
+        res = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                            q_pos_offset=q_pos_offset, window_left=window_left,
+                            window_right=window_right, softcap=softcap, alibi=alibi,
+                            return_lse=return_lse, bias=bias)
+        if return_lse:
+            return _wrap_grad(res[0], q, k, v), res[1]
+        return _wrap_grad(res, q, k, v)
+    out, lse = _DenseAttention.apply(q, k, v, softmax_scale, causal, q_pos_offset, window_left,
+                                     window_right, softcap, alibi)
+    return (out, lse) if return_lse else out
+
+
+def varlen_attention(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
+                     softmax_scale: float, causal: bool, window_left: int = -1,
+                     window_right: int = -1, softcap: float = 0.0,
+                     alibi: Optional[torch.Tensor] = None, return_lse: bool = False):
+    """``varlen_forward`` that is differentiable in q, k, v (fp16 / bf16)."""
+    if not _needs_grad(q, k, v):
+        return varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
+                              softmax_scale=softmax_scale, causal=causal,
+                              window_left=window_left, window_right=window_right,
+                              softcap=softcap, alibi=alibi, return_lse=return_lse)
+    out, lse = _VarlenAttention.apply(q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
+                                      softmax_scale, causal, window_left, window_right, softcap,
+                                      alibi)
+    return (out, lse) if return_lse else out
+
+
 def attention(q, k, v, causal=False, sm_scale=None, dropout_p=0.0, dropout_seed=None,
               seq_len_k=None, seq_len_q=None, kv_heads=None, softcap=0.0, alibi_slopes=None,
               window_left=-1, window_right=-1, use_alibi=None):
@@ -155,11 +312,11 @@ def attention(q, k, v, causal=False, sm_scale=None, dropout_p=0.0, dropout_seed=
     alibi = None
     if use_alibi:
         alibi = alibi_slopes.reshape(-1, q.shape[1]).expand(q.shape[0], -1)
-    out = dense_forward(
+    out = dense_attention(
         q.transpose(1, 2), k.transpose(1, 2)[:, :seq_len_k], v.transpose(1, 2)[:, :seq_len_k],
         softmax_scale=sm_scale, causal=causal, q_pos_offset=seq_len_k - seq_len_q,
         window_left=window_left, window_right=window_right, softcap=softcap, alibi=alibi)
-    return _wrap_grad(out.transpose(1, 2), q, k, v)
+    return out.transpose(1, 2)
 
 
 def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
@@ -174,8 +331,7 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
         use_alibi = False
     elif use_alibi is None:
         use_alibi = bool(torch.any(alibi_slopes != 0))
-    out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                         softmax_scale=sm_scale, causal=causal, window_left=window_left,
-                         window_right=window_right, softcap=softcap,
-                         alibi=alibi_slopes if use_alibi else None)
-    return _wrap_grad(out, q, k, v)
+    return varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                            softmax_scale=sm_scale, causal=causal, window_left=window_left,
+                            window_right=window_right, softcap=softcap,
+                            alibi=alibi_slopes if use_alibi else None)

@@ -108,6 +108,48 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
                   fa_stream_t stream);
 
+/* Backward of fa_fwd_dense: dq, dk, dv from dout.
+ *
+ * Replaces `_dense_backward` (attention_kernel.py:1104-1155: the
+ * `_attn_bwd_preprocess` and `_attn_bwd` launches, :536-566 and :809-1054).
+ * q, k, v, out, dout, dq, dk, dv are [B, S, H, D] with *_stride[3] = {batch,
+ * seq, head} (k, v, dk, dv with Hk heads); lse is the natural-log LSE the
+ * forward returned ([B, Hq, Sq] at lse_stride {batch, head, seq}); delta is an
+ * fp32 workspace of the same shape and strides (written, then read).  The
+ * score options (scale, causal, q_pos_offset, window, softcap, ALiBi) must be
+ * those of the forward call.  dq / dk / dv are written, not accumulated; grouped
+ * KV heads are reduced inside the kernel (no atomics, deterministic).  dtype
+ * fp16 or bf16; head_dim 32, 64, 128 or 256.  Launches two kernels on
+ * `stream`.
+ */
+int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                 const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
+                 int64_t seqlen_q, int64_t seqlen_k, int64_t heads_q, int64_t heads_k,
+                 int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                 const int64_t* v_stride, const int64_t* o_stride, const int64_t* do_stride,
+                 const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
+                 const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                 int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
+                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream);
+
+/* Backward of fa_fwd_varlen (without seqused / block table).
+ *
+ * Replaces `_attention_varlen.backward` (attention_kernel.py:1322-1361: the
+ * `_varlen_bwd` and `_varlen_bwd_dkdv` launches, :107-272).  Packed tensors
+ * with *_stride[2] = {token, head}; lse / delta [Tq, Hq] at lse_stride
+ * {token, head}.  Other arguments as fa_bwd_dense.
+ */
+int fa_bwd_varlen(const void* q, const void* k, const void* v, const void* out,
+                  const void* dout, const float* lse, void* dq, void* dk, void* dv, float* delta,
+                  const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int64_t heads_q, int64_t heads_k,
+                  int64_t head_dim, const int64_t* q_stride, const int64_t* k_stride,
+                  const int64_t* v_stride, const int64_t* o_stride, const int64_t* do_stride,
+                  const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
+                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                  int64_t window_left, int64_t window_right, float softcap,
+                  const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream);
+
 /* Split-KV plan for fa_fwd_kvcache: the number of key splits the launch will
  * use and the workspace bytes it needs (0 when num_splits == 1).
  * max_keys bounds every sequence's visible key count (e.g. the cache

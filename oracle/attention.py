@@ -35,7 +35,9 @@ import numpy as np
 
 __all__ = [
     "attention",
+    "attention_backward",
     "attention_varlen",
+    "attention_varlen_backward",
     "attention_kvcache",
     "gather_paged_kv",
     "compact_varlen",
@@ -109,6 +111,56 @@ def attention(q, k, v, softmax_scale: Optional[float] = None, causal: bool = Fal
     return out, lse, probs
 
 
+def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
+                       causal: bool = False, window_size: Sequence[int] = (-1, -1),
+                       softcap: float = 0.0, alibi_slopes=None, causal_offset: int = 0
+                       ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Exact gradients ``(dq, dk, dv)`` of :func:`attention`'s output against
+    ``dout [B,Sq,Hq,D]``, in float64.
+
+    The chain rule through the score pipeline, as the reference's backward
+    kernels compute it (attention_kernel.py:569-668 dK/dV, :671-776 dQ,
+    :536-566 delta; the reference's math path :15-49 is differentiated by
+    torch autograd the same way): ``dV = P^T dO``, ``dP = dO V^T``,
+    ``delta = rowsum(dO * O)``, ``dS = P (dP - delta) (1 - tanh^2)`` (the last
+    factor only with softcap), ``dQ = scale dS K``, ``dK = scale dS^T Q``;
+    grouped KV heads sum the gradients of their query heads.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    dout = np.asarray(dout, dtype=np.float64)
+    batch, q_len, q_heads, head_dim = q.shape
+    k_len, kv_heads = k.shape[1], k.shape[2]
+    rep = q_heads // kv_heads
+    scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
+    out, _, probs = attention(q, k, v, scale, causal, window_size, softcap, alibi_slopes,
+                              None, causal_offset)
+    kr = np.repeat(k, rep, axis=2).transpose(0, 2, 1, 3)     # [B,H,Sk,D]
+    vr = np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)
+    qh = q.transpose(0, 2, 1, 3)                              # [B,H,Sq,D]
+    doh = dout.transpose(0, 2, 1, 3)
+    dv_h = np.matmul(probs.transpose(0, 1, 3, 2), doh)        # [B,H,Sk,D]
+    dp = np.matmul(doh, vr.transpose(0, 1, 3, 2))             # [B,H,Sq,Sk]
+    delta = np.sum(doh * out.transpose(0, 2, 1, 3), axis=-1, keepdims=True)
+    ds = probs * (dp - delta)
+    if softcap > 0:
+        raw = np.matmul(qh, kr.transpose(0, 1, 3, 2)) * scale
+        if alibi_slopes is not None:
+            slopes = np.asarray(alibi_slopes, dtype=np.float64)
+            if slopes.ndim == 1:
+                slopes = slopes[None, :]
+            q_pos = np.arange(q_len) + int(causal_offset)
+            dist = np.abs(q_pos[:, None] - np.arange(k_len)[None, :]).astype(np.float64)
+            raw = raw - slopes[:, :, None, None] * dist[None, None]
+        ds = ds * (1.0 - np.tanh(raw / softcap) ** 2)
+    dq = (np.matmul(ds, kr) * scale).transpose(0, 2, 1, 3)
+    dk_h = np.matmul(ds.transpose(0, 1, 3, 2), qh) * scale
+    dk = dk_h.reshape(batch, kv_heads, rep, k_len, head_dim).sum(axis=2).transpose(0, 2, 1, 3)
+    dv = dv_h.reshape(batch, kv_heads, rep, k_len, head_dim).sum(axis=2).transpose(0, 2, 1, 3)
+    return dq, dk, dv
+
+
 def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, causal=False,
                      window_size=(-1, -1), softcap=0.0, alibi_slopes=None
                      ) -> Tuple[np.ndarray, np.ndarray]:
@@ -147,6 +199,36 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, ca
         out[qs:qe] = o[0]
         lse[qs:qe] = l[0].T
     return out, lse
+
+
+def attention_varlen_backward(q, k, v, dout, cu_seqlens_q, cu_seqlens_k, softmax_scale=None,
+                              causal=False, window_size=(-1, -1), softcap=0.0,
+                              alibi_slopes=None) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Gradients of :func:`attention_varlen`: :func:`attention_backward` per
+    sequence (attention_kernel.py:107-272); rows outside every sequence get
+    zero gradients."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    dout = np.asarray(dout, dtype=np.float64)
+    cu_q = np.asarray(cu_seqlens_q, dtype=np.int64)
+    cu_k = np.asarray(cu_seqlens_k, dtype=np.int64)
+    batch = cu_q.shape[0] - 1
+    dq, dk, dv = np.zeros(q.shape), np.zeros(k.shape), np.zeros(v.shape)
+    slopes = None
+    if alibi_slopes is not None:
+        slopes = np.asarray(alibi_slopes, dtype=np.float64)
+        if slopes.ndim == 1:
+            slopes = np.broadcast_to(slopes[None, :], (batch, q.shape[1]))
+    for b in range(batch):
+        qs, qe, ks, ke = int(cu_q[b]), int(cu_q[b + 1]), int(cu_k[b]), int(cu_k[b + 1])
+        if qe == qs or ke == ks:
+            continue
+        g = attention_backward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke],
+                               dout[None, qs:qe], softmax_scale, causal, window_size, softcap,
+                               None if slopes is None else slopes[b:b + 1])
+        dq[qs:qe], dk[ks:ke], dv[ks:ke] = g[0][0], g[1][0], g[2][0]
+    return dq, dk, dv
 
 
 def gather_paged_kv(cache, block_table_row, length: int, start: int = 0) -> np.ndarray:

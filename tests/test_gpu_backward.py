@@ -1,0 +1,202 @@
+"""Gradients of the HIP backward kernels (fa_bwd_dense / fa_bwd_varlen) against
+the float64 oracle (oracle/attention.py attention_backward, pinned against
+torch autograd and finite differences in tests/test_oracle.py).
+
+Bars: the reference's own gradient tests compare fp16 against SDPA at
+atol = rtol = 2e-2 (tests/test_compare_implementations.py:23-24,81-82).  Here
+the comparison is against the exact float64 gradient, elementwise
+|got - exact| <= GRAD_ATOL + GRAD_RTOL * |exact|: fp16 inputs carry P and dS
+rounded to fp16 into fp32 accumulations, bf16 rounds them 8x coarser.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _helpers import randn, to_np
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+GRAD_ATOL = {torch.float16: 5e-3, torch.bfloat16: 4e-2}
+GRAD_RTOL = {torch.float16: 1e-2, torch.bfloat16: 4e-2}
+
+
+def _check(name, got, exact, dtype):
+    got = to_np(got.cpu())
+    err = np.abs(got - exact)
+    bound = GRAD_ATOL[dtype] + GRAD_RTOL[dtype] * np.abs(exact)
+    worst = float(np.max(err - bound)) if err.size else -1.0
+    assert np.all(np.isfinite(got)), f"{name}: non-finite gradient"
+    assert worst <= 0, (f"{name}: max |err| {float(np.max(err)):.3e} exceeds the bar "
+                        f"(max |exact| {float(np.max(np.abs(exact))):.3e})")
+
+
+def _dense_case(B, Sq, Sk, Hq, Hk, D, dtype=torch.float16, seed=0, causal=False,
+                window=(-1, -1), softcap=0.0, alibi=False, scale=None, api="func"):
+    from flash_attn_triton import flash_attn_func, flash_attn_func_cross
+    q = randn((B, Sq, Hq, D), seed + 1, dtype)
+    k = randn((B, Sk, Hk, D), seed + 2, dtype)
+    v = randn((B, Sk, Hk, D), seed + 3, dtype)
+    do = randn((B, Sq, Hq, D), seed + 4, dtype)
+    slopes = (torch.rand(Hq, generator=torch.Generator().manual_seed(seed + 5)) * 0.5
+              if alibi else None)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    fn = flash_attn_func if (api == "func" and Sq == Sk) else flash_attn_func_cross
+    out = fn(qd, kd, vd, causal=causal, window_size=window, softcap=softcap,
+             alibi_slopes=None if slopes is None else slopes.to(DEV), softmax_scale=scale)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    ref = ora.attention_backward(to_np(q), to_np(k), to_np(v), to_np(do), scale, causal, window,
+                                 softcap, None if slopes is None else slopes.double().numpy())
+    for name, t, r in zip(("dq", "dk", "dv"), (qd, kd, vd), ref):
+        _check(name, t.grad, r, dtype)
+    return qd.grad, kd.grad, vd.grad
+
+
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
+@pytest.mark.parametrize("causal", [False, True])
+def test_head_dims(d, causal):
+    _dense_case(2, 200, 200, 4, 4, d, causal=causal, seed=d)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_gqa_ragged_lengths(dtype, causal):
+    _dense_case(2, 333, 333, 8, 2, 128, dtype=dtype, causal=causal, seed=11)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_cross_lengths(causal):
+    # Sq != Sk: flash_attn_func_cross, upper-left alignment.
+    _dense_case(1, 70, 301, 4, 2, 64, causal=causal, seed=21)
+    _dense_case(1, 257, 64, 4, 4, 128, causal=causal, seed=22)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_window_alibi_softcap(d):
+    _dense_case(2, 300, 300, 4, 2, d, causal=True, window=(64, 0), softcap=20.0, alibi=True,
+                seed=31)
+    _dense_case(1, 190, 190, 2, 1, d, causal=False, window=(16, 40), softcap=5.0, seed=32,
+                scale=0.3)
+
+
+def test_d256_generic():
+    _dense_case(1, 150, 150, 2, 2, 256, causal=True, softcap=10.0, alibi=True, seed=41)
+
+
+def test_reference_gradient_case():
+    # tests/test_compare_implementations.py:86-91: B2 S17 H2 D16, scale 0.125.
+    for causal in (False, True):
+        _dense_case(2, 17, 17, 2, 2, 16, causal=causal, scale=0.125, seed=42)
+
+
+def test_deterministic():
+    a = _dense_case(1, 256, 256, 8, 2, 64, causal=True, seed=51)
+    b = _dense_case(1, 256, 256, 8, 2, 64, causal=True, seed=51)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y), "two identical backward calls differ"
+
+
+def test_qkvpacked_and_low_level_attention():
+    from flash_attn_triton import flash_attn_qkvpacked_func
+    from flash_attn_triton.triton_kernel.attention_kernel import attention
+    qkv = randn((1, 128, 3, 2, 64), 61).to(DEV).requires_grad_()
+    do = randn((1, 128, 2, 64), 62).to(DEV)
+    flash_attn_qkvpacked_func(qkv, causal=True).backward(do)
+    q, k, v = (to_np(t) for t in qkv.detach().cpu().unbind(2))
+    ref = ora.attention_backward(q, k, v, to_np(do.cpu()), None, True)
+    for i in range(3):
+        _check(f"dqkv[{i}]", qkv.grad[:, :, i], ref[i], torch.float16)
+    # attention(): [B, H, S, D] views, the reference's low-level entry point.
+    qh, kh, vh = (randn((1, 2, 128, 64), s).to(DEV).requires_grad_() for s in (63, 64, 65))
+    attention(qh, kh, vh, causal=True).backward(do.transpose(1, 2))
+    ref = ora.attention_backward(*(to_np(t.detach().cpu().transpose(1, 2)) for t in (qh, kh, vh)),
+                                 to_np(do.cpu()), None, True)
+    for name, t, r in zip(("dq", "dk", "dv"), (qh, kh, vh), ref):
+        _check(name, t.grad.transpose(1, 2), r, torch.float16)
+
+
+def test_probs_path_gradients():
+    from flash_attn_triton import flash_attn_func
+    q, k, v = (randn((1, 96, 2, 32), s).to(DEV).requires_grad_() for s in (71, 72, 73))
+    do = randn((1, 96, 2, 32), 74)
+    out, lse, probs = flash_attn_func(q, k, v, causal=True, return_attn_probs=True)
+    assert not lse.requires_grad and not probs.requires_grad
+    out.backward(do.to(DEV))
+    ref = ora.attention_backward(*(to_np(t.detach().cpu()) for t in (q, k, v)), to_np(do),
+                                 None, True)
+    for name, t, r in zip(("dq", "dk", "dv"), (q, k, v), ref):
+        _check(name, t.grad, r, torch.float16)
+
+
+def _varlen_case(lq, lk, Hq=4, Hk=2, D=64, dtype=torch.float16, seed=0, causal=False,
+                 window=(-1, -1), softcap=0.0, alibi=False):
+    from flash_attn_triton import flash_attn_varlen_func
+    cq = torch.tensor(np.concatenate([[0], np.cumsum(lq)]), dtype=torch.int32)
+    ck = torch.tensor(np.concatenate([[0], np.cumsum(lk)]), dtype=torch.int32)
+    q = randn((int(sum(lq)), Hq, D), seed + 1, dtype)
+    k = randn((int(sum(lk)), Hk, D), seed + 2, dtype)
+    v = randn((int(sum(lk)), Hk, D), seed + 3, dtype)
+    do = randn((int(sum(lq)), Hq, D), seed + 4, dtype)
+    slopes = (torch.rand(len(lq), Hq, generator=torch.Generator().manual_seed(seed + 5)) * 0.5
+              if alibi else None)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = flash_attn_varlen_func(qd, kd, vd, cq.to(DEV), ck.to(DEV), max(lq), max(lk),
+                                 causal=causal, window_size=window, softcap=softcap,
+                                 alibi_slopes=None if slopes is None else slopes.to(DEV))
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    ref = ora.attention_varlen_backward(to_np(q), to_np(k), to_np(v), to_np(do), cq.numpy(),
+                                        ck.numpy(), None, causal, window, softcap,
+                                        None if slopes is None else slopes.double().numpy())
+    for name, t, r in zip(("dq", "dk", "dv"), (qd, kd, vd), ref):
+        _check(name, t.grad, r, dtype)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_ragged(causal):
+    _varlen_case([1, 130, 64, 257, 5], [3, 130, 200, 100, 5], causal=causal, seed=80)
+
+
+def test_varlen_empty_sequences_and_features():
+    _varlen_case([0, 20, 33, 7], [5, 0, 40, 7], causal=True, seed=90)
+    _varlen_case([300, 129, 64], [300, 129, 64], Hq=8, Hk=2, D=128, causal=True,
+                 window=(64, 0), softcap=30.0, alibi=True, seed=91)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_varlen_dtypes_d128(dtype):
+    _varlen_case([200, 513], [200, 513], Hq=4, Hk=4, D=128, dtype=dtype, causal=True, seed=95)
+
+
+def test_baseline_c2_sampled_heads():
+    # BASELINE config 2 shape (B4 H32 S4096 D128 fp16, causal): the whole
+    # backward runs; two (batch, head) slices are checked against the oracle.
+    from flash_attn_triton import flash_attn_func
+    B, S, H, D = 4, 4096, 32, 128
+    gen = torch.Generator(device="cpu").manual_seed(1)
+    q, k, v, do = (torch.randn((B, S, H, D), generator=gen).to(torch.float16) for _ in range(4))
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    flash_attn_func(qd, kd, vd, causal=True).backward(do.to(DEV))
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (3, 31)):
+        sl = (slice(b, b + 1), slice(None), slice(h, h + 1))
+        ref = ora.attention_backward(to_np(q[sl]), to_np(k[sl]), to_np(v[sl]), to_np(do[sl]),
+                                     None, True)
+        for name, t, r in zip(("dq", "dk", "dv"), (qd, kd, vd), ref):
+            _check(f"{name}[{b},{h}]", t.grad[sl], r, torch.float16)
+
+
+def test_forward_only_paths_raise_on_backward():
+    from flash_attn_triton import flash_attn_func
+    q = randn((1, 64, 2, 64), 100, torch.float32).to(DEV).requires_grad_()
+    out = flash_attn_func(q, q, q)
+    with pytest.raises(NotImplementedError):
+        out.sum().backward()
+    q16 = randn((1, 64, 2, 64), 101).to(DEV).requires_grad_()
+    out = flash_attn_func(q16, q16, q16, attn_bias=torch.zeros((64, 64), device=DEV))
+    with pytest.raises(NotImplementedError):
+        out.sum().backward()

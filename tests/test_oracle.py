@@ -277,6 +277,92 @@ def test_compact_varlen_seqused_is_truncated_per_sequence_sdpa():
     assert out.shape[0] == sum(uq)
 
 
+# ----------------------------------------------------------------- gradients
+def _torch_math(q, k, v, scale, causal, window, softcap, slopes, offset):
+    """The reference's math path (flash_attn_interface.py:15-49) in float64 torch,
+    for autograd: BSHD inputs, GQA by repeat_interleave."""
+    rep = q.shape[2] // k.shape[2]
+    k = k.repeat_interleave(rep, dim=2)
+    v = v.repeat_interleave(rep, dim=2)
+    s = torch.einsum("bqhd,bkhd->bhqk", q, k) * scale
+    qp = torch.arange(q.shape[1], dtype=torch.float64)[:, None] + offset
+    kp = torch.arange(k.shape[1], dtype=torch.float64)[None, :]
+    if slopes is not None:
+        s = s - slopes[None, :, None, None] * (qp - kp).abs()
+    if softcap > 0:
+        s = softcap * torch.tanh(s / softcap)
+    keep = torch.ones_like(qp * kp, dtype=torch.bool)
+    if causal:
+        keep &= qp >= kp
+    if window[0] >= 0:
+        keep &= kp >= qp - window[0]
+    if window[1] >= 0:
+        keep &= kp <= qp + window[1]
+    p = torch.nan_to_num(torch.softmax(s.masked_fill(~keep, float("-inf")), dim=-1))
+    return torch.einsum("bhqk,bkhd->bqhd", p, v)
+
+
+@pytest.mark.parametrize("case", [
+    dict(causal=False, window=(-1, -1), softcap=0.0, alibi=False, offset=0, sq=9, sk=9),
+    dict(causal=True, window=(-1, -1), softcap=0.0, alibi=False, offset=0, sq=9, sk=12),
+    dict(causal=True, window=(3, 0), softcap=5.0, alibi=True, offset=3, sq=7, sk=10),
+    dict(causal=False, window=(2, 1), softcap=2.0, alibi=True, offset=0, sq=8, sk=8),
+])
+def test_backward_matches_torch_autograd(case):
+    rng = np.random.default_rng(50)
+    B, Hq, Hk, D = 2, 4, 2, 8
+    q = rng.standard_normal((B, case["sq"], Hq, D))
+    k = rng.standard_normal((B, case["sk"], Hk, D))
+    v = rng.standard_normal((B, case["sk"], Hk, D))
+    do = rng.standard_normal((B, case["sq"], Hq, D))
+    slopes = rng.uniform(0.1, 0.9, Hq) if case["alibi"] else None
+    tq, tk, tv = (torch.from_numpy(x).requires_grad_() for x in (q, k, v))
+    out = _torch_math(tq, tk, tv, 0.3, case["causal"], case["window"], case["softcap"],
+                      None if slopes is None else torch.from_numpy(slopes), case["offset"])
+    out.backward(torch.from_numpy(do))
+    got = ora.attention_backward(q, k, v, do, 0.3, case["causal"], case["window"],
+                                 case["softcap"], slopes, case["offset"])
+    for g, t in zip(got, (tq, tk, tv)):
+        np.testing.assert_allclose(g, t.grad.numpy(), atol=1e-12)
+
+
+def test_backward_matches_finite_differences():
+    # d/dx of sum(out * dout) by central differences, every input element.
+    rng = np.random.default_rng(51)
+    q, k, v = rng.standard_normal((1, 4, 2, 4)), rng.standard_normal((1, 5, 1, 4)), \
+        rng.standard_normal((1, 5, 1, 4))
+    do = rng.standard_normal((1, 4, 2, 4))
+    kw = dict(softmax_scale=0.7, causal=True, window_size=(2, -1), softcap=3.0,
+              alibi_slopes=np.array([0.25, 0.5]), causal_offset=1)
+    grads = ora.attention_backward(q, k, v, do, **kw)
+    f = lambda a, b, c: float(np.sum(ora.attention(a, b, c, **kw)[0] * do))
+    h = 1e-6
+    for idx, x in enumerate((q, k, v)):
+        num = np.zeros_like(x)
+        for pos in np.ndindex(x.shape):
+            args = [q.copy(), k.copy(), v.copy()]
+            args[idx][pos] += h
+            fp = f(*args)
+            args[idx][pos] -= 2 * h
+            num[pos] = (fp - f(*args)) / (2 * h)
+        np.testing.assert_allclose(grads[idx], num, atol=1e-7)
+
+
+def test_varlen_backward_is_per_sequence_backward():
+    rng = np.random.default_rng(52)
+    q, k, v = rng.standard_normal((9, 2, 8)), rng.standard_normal((11, 2, 8)), \
+        rng.standard_normal((11, 2, 8))
+    do = rng.standard_normal((9, 2, 8))
+    dq, dk, dv = ora.attention_varlen_backward(q, k, v, do, [0, 4, 4, 9], [0, 5, 6, 11],
+                                               causal=True)
+    g0 = ora.attention_backward(q[None, :4], k[None, :5], v[None, :5], do[None, :4], causal=True)
+    g2 = ora.attention_backward(q[None, 4:], k[None, 6:], v[None, 6:], do[None, 4:], causal=True)
+    np.testing.assert_allclose(dq, np.concatenate([g0[0][0], g2[0][0]]), atol=1e-14)
+    np.testing.assert_allclose(dk, np.concatenate([g0[1][0], np.zeros((1, 2, 8)), g2[1][0]]),
+                               atol=1e-14)
+    np.testing.assert_allclose(dv[5], 0.0)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_kvcache_decode_matches_sdpa_bottom_right(causal):
     rng = np.random.default_rng(41)
