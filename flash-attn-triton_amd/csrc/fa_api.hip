@@ -3,6 +3,7 @@
 // Each entry point validates its arguments, fills a kernel parameter block
 // and launches on the caller's stream.  Nothing here allocates device memory
 // or synchronizes.
+#include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -81,7 +82,20 @@ void fill_scale(fa::FwdParams& p, float scale, float softcap, const float* alibi
 }
 
 bool needs_generic(const fa::FwdParams& p) {
-  return p.alibi != nullptr || p.softcap > 0.f || !(p.scale > 0.f);
+  return p.alibi != nullptr || p.softcap > 0.f || !(p.scale > 0.f) || p.drop.enabled;
+}
+
+// Dropout of probability p with a 64-bit seed (the mask is defined in
+// fa_common.h); p = 0 disables it.
+bool fill_dropout(fa::DropoutCfg& d, float p, uint64_t seed) {
+  if (!(p >= 0.f && p < 1.f)) return false;
+  d.enabled = p > 0.f;
+  d.seed_lo = (uint32_t)(seed & 0xffffffffu);
+  d.seed_hi = (uint32_t)(seed >> 32);
+  d.t16 = (int)nearbyint((double)p * 65536.0);
+  if (d.t16 > 65536) d.t16 = 65536;
+  d.scale = (float)(1.0 / (1.0 - (double)p));
+  return true;
 }
 
 struct KvPlan {
@@ -154,7 +168,9 @@ namespace {
 int bwd_launch(const char* name, fa::BwdParams& p, int dtype, int64_t head_dim,
                float softmax_scale, float softcap, const float* alibi_slopes,
                int64_t alibi_batch_stride, int causal, int64_t window_left, int64_t window_right,
-               hipStream_t st) {
+               float dropout_p, uint64_t dropout_seed, hipStream_t st) {
+  if (!fill_dropout(p.drop, dropout_p, dropout_seed))
+    return fail(FA_ERR_INVALID, "%s: dropout_p must be in [0, 1)", name);
   p.scale = softmax_scale;
   p.scale_log2 = softmax_scale * fa::kLog2e;
   p.softcap = softcap;
@@ -164,7 +180,7 @@ int bwd_launch(const char* name, fa::BwdParams& p, int dtype, int64_t head_dim,
   p.causal = causal != 0;
   p.window_left = clamp_window(window_left);
   p.window_right = clamp_window(window_right);
-  const bool generic = alibi_slopes != nullptr || softcap > 0.f;
+  const bool generic = alibi_slopes != nullptr || softcap > 0.f || p.drop.enabled;
   const hipError_t e = dtype == FA_DTYPE_F16 ? fa_launch_bwd_f16(p, (int)head_dim, generic, st)
                                              : fa_launch_bwd_bf16(p, (int)head_dim, generic, st);
   return hip_status(e, name);
@@ -202,7 +218,8 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
                  const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
-                 const int64_t* bias_stride, fa_stream_t stream) {
+                 const int64_t* bias_stride, float dropout_p, uint64_t dropout_seed,
+                 fa_stream_t stream) {
   if (!q || !k || !v || !out || !q_stride || !k_stride || !v_stride || !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_dense: null pointer argument");
   if (attn_bias && !bias_stride)
@@ -247,6 +264,8 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
     p.bias_sb = bias_stride[0]; p.bias_sh = bias_stride[1];
     p.bias_sq = bias_stride[2]; p.bias_sk = bias_stride[3];
   }
+  if (!fill_dropout(p.drop, dropout_p, dropout_seed))
+    return fail(FA_ERR_INVALID, "fa_fwd_dense: dropout_p must be in [0, 1)");
   p.num_splits = 1;
   p.heavy_first = p.causal || p.window_right >= 0;
   return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim,
@@ -264,7 +283,7 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   int64_t alibi_batch_stride, const int32_t* seqused_q,
                   const int32_t* seqused_k, const int32_t* cu_seqlens_out,
                   const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
-                  fa_stream_t stream) {
+                  float dropout_p, uint64_t dropout_seed, fa_stream_t stream) {
   if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k || !q_stride || !k_stride ||
       !v_stride || !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_varlen: null pointer argument");
@@ -303,6 +322,8 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
   if (lse) { p.lse_ss = lse_stride[0]; p.lse_sh = lse_stride[1]; }
   p.cu_q = cu_seqlens_q; p.cu_k = cu_seqlens_k;
   p.seqused_q = seqused_q; p.seqused_k = seqused_k; p.cu_o = cu_seqlens_out;
+  if (!fill_dropout(p.drop, dropout_p, dropout_seed))
+    return fail(FA_ERR_INVALID, "fa_fwd_varlen: dropout_p must be in [0, 1)");
   p.batch = (int)batch; p.seqlen_q = (int)max_seqlen_q; p.seqlen_k = (int)max_seqlen_k;
   p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
   fill_scale(p, softmax_scale, softcap, alibi_slopes);
@@ -325,7 +346,8 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
                  const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
-                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream) {
+                 const float* alibi_slopes, int64_t alibi_batch_stride, float dropout_p,
+                 uint64_t dropout_seed, fa_stream_t stream) {
   const char* name = "fa_bwd_dense";
   int rc = bwd_check_common(name, q, k, v, out, dout, lse, dq, dk, dv, delta, dtype, head_dim,
                             heads_q, heads_k);
@@ -361,7 +383,8 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
   p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
   p.q_offset = q_pos_offset;
   return bwd_launch(name, p, dtype, head_dim, softmax_scale, softcap, alibi_slopes,
-                    alibi_batch_stride, causal, window_left, window_right, (hipStream_t)stream);
+                    alibi_batch_stride, causal, window_left, window_right, dropout_p,
+                    dropout_seed, (hipStream_t)stream);
 }
 
 int fa_bwd_varlen(const void* q, const void* k, const void* v, const void* out,
@@ -373,7 +396,8 @@ int fa_bwd_varlen(const void* q, const void* k, const void* v, const void* out,
                   const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                   int64_t window_left, int64_t window_right, float softcap,
-                  const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream) {
+                  const float* alibi_slopes, int64_t alibi_batch_stride, float dropout_p,
+                  uint64_t dropout_seed, fa_stream_t stream) {
   const char* name = "fa_bwd_varlen";
   int rc = bwd_check_common(name, q, k, v, out, dout, lse, dq, dk, dv, delta, dtype, head_dim,
                             heads_q, heads_k);
@@ -407,7 +431,8 @@ int fa_bwd_varlen(const void* q, const void* k, const void* v, const void* out,
   p.batch = (int)batch; p.seqlen_q = (int)max_seqlen_q; p.seqlen_k = (int)max_seqlen_k;
   p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
   return bwd_launch(name, p, dtype, head_dim, softmax_scale, softcap, alibi_slopes,
-                    alibi_batch_stride, causal, window_left, window_right, (hipStream_t)stream);
+                    alibi_batch_stride, causal, window_left, window_right, dropout_p,
+                    dropout_seed, (hipStream_t)stream);
 }
 
 int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_t heads_k,
@@ -542,7 +567,8 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                   int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
                   const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
-                  const int64_t* bias_stride, fa_stream_t stream) {
+                  const int64_t* bias_stride, float dropout_p, uint64_t dropout_seed,
+                  fa_stream_t stream) {
   if (!q || !k || !lse || !probs || !q_stride || !k_stride || !lse_stride)
     return fail(FA_ERR_INVALID, "fa_attn_probs: null pointer argument");
   if ((cu_seqlens_q == nullptr) != (cu_seqlens_k == nullptr))
@@ -583,6 +609,8 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
   p.causal = causal != 0; p.q_offset = (int)q_pos_offset;
   p.window_left = clamp_window(window_left);
   p.window_right = clamp_window(window_right);
+  if (!fill_dropout(p.drop, dropout_p, dropout_seed))
+    return fail(FA_ERR_INVALID, "fa_attn_probs: dropout_p must be in [0, 1)");
   return hip_status(fa_launch_probs(dtype, p, (hipStream_t)stream), "fa_attn_probs launch");
 }
 

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fa_common.h"
+
 namespace fa {
 
 // All strides are in elements.  Layouts as in the forward:
@@ -31,6 +33,7 @@ struct BwdParams {
   int causal, window_left, window_right;
   int64_t q_offset;                               // query row i sits at position i + q_offset
   const int* cu_q; const int* cu_k;
+  DropoutCfg drop;                                // the forward's dropout (GENERIC only)
   int n_blocks, total_blocks;                     // filled by the launcher
 };
 

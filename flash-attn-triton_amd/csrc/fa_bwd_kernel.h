@@ -9,7 +9,10 @@
 //   dS = P * (dP - delta) * softcap'          (softcap' = 1 - tanh^2, else 1)
 //   dQ = scale * dS K        dK = scale * dS^T Q
 // with the forward's natural-log LSE, so P is exactly the forward's
-// probabilities (rows with no visible key have LSE = -inf and P = 0).
+// probabilities (rows with no visible key have LSE = -inf and P = 0).  With
+// dropout (multipliers F of fa_common.h's mask): dV = (F P)^T dO and
+// dS = P (F dP - delta) -- the derivative of O = (F P) V, where the
+// reference's kernels use F P (dP - delta) (attention_kernel.py:661, :763).
 //
 // Two kernels, no atomics, deterministic:
 // * bwd_dq_kernel: a workgroup owns BM = 32*NW query rows of one (batch,
@@ -282,10 +285,13 @@ void bwd_dq_kernel(const BwdParams p) {
       }
     }
     const int n0 = t * BN;
+    const bool drop = GENERIC && p.drop.enabled;
     u32x4 dsb[NCC];
 #pragma unroll
     for (int cc = 0; cc < NCC; ++cc) {
       const int kb = cc >> 1, o8 = (cc & 1) * 8;
+      u32x4 rnd = {0, 0, 0, 0};
+      if (drop) rnd = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float ds[2];
@@ -296,7 +302,8 @@ void bwd_dq_kernel(const BwdParams p) {
           float cg;
           float pr = bwd_prob<GENERIC>(p, s[kb][v], lse2, slope, qpos, key, cg);
           if (masked && (key < key_lo || key > key_hi)) pr = 0.f;
-          ds[u] = pr * (dp[kb][v] - delta) * cg;
+          const float dpv = drop ? dp[kb][v] * dropout_factor(p.drop, rnd, 2 * j + u) : dp[kb][v];
+          ds[u] = pr * (dpv - delta) * cg;
         }
         dsb[cc][j] = T::pack2(ds[0], ds[1]);
       }
@@ -555,8 +562,14 @@ void bwd_dkdv_kernel(const BwdParams p) {
             if (wl >= 0) vis = vis && kj >= qpos - wl;
             if (!vis) pr = 0.f;
           }
+          float dpv = dp[rb][v];
           pv[u] = pr;
-          ds[u] = pr * (dp[rb][v] - dl) * cg;
+          if (GENERIC && p.drop.enabled) {
+            const float f = dropout_factor_at(p.drop, row, kj, hq, b);
+            pv[u] = pr * f;
+            dpv *= f;
+          }
+          ds[u] = pr * (dpv - dl) * cg;
         }
         pb[cc][j] = T::pack2(pv[0], pv[1]);
         dsb[cc][j] = T::pack2(ds[0], ds[1]);

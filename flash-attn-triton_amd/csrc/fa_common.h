@@ -134,4 +134,64 @@ __device__ inline uint32_t rows_extent(int row0, int rows, int64_t row_stride, i
   return bytes > 0xffffffffll ? 0xffffffffu : (uint32_t)bytes;
 }
 
+// ------------------------------------------------------------------ dropout
+// Counter-based random bits: Philox4x32-10 (Salmon, Moraes, Dror and Shaw,
+// "Parallel random numbers: as easy as 1, 2, 3", SC 2011; the Random123
+// reference parameters).  One call maps a 128-bit counter and a 64-bit key to
+// 128 random bits.
+__device__ inline u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1) {
+  constexpr uint32_t kM0 = 0xD2511F53u, kM1 = 0xCD9E8D57u;
+  constexpr uint32_t kW0 = 0x9E3779B9u, kW1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    if (r) {
+      k0 += kW0;
+      k1 += kW1;
+    }
+    const uint64_t p0 = (uint64_t)kM0 * c[0];
+    const uint64_t p1 = (uint64_t)kM1 * c[2];
+    c = u32x4{(uint32_t)(p1 >> 32) ^ c[1] ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c[3] ^ k1,
+              (uint32_t)p0};
+  }
+  return c;
+}
+
+// Dropout mask.  Element (batch b, query head h, query row i, key j; rows and
+// keys local to the sequence) keeps its probability iff its 16-bit draw is at
+// least t16 = round(p * 65536), and a kept probability is scaled by
+// 1 / (1 - p).  The draws come 8 to a Philox call: call
+// (2 (j / 16) + (j / 4) % 2, i, h, b) under key (seed_lo, seed_hi) covers the
+// keys 16 (j / 16) + 4 s + {0, 1, 2, 3, 8, 9, 10, 11} (s = (j / 4) % 2) in the
+// order of its eight 16-bit halves, word e / 2 bits 16 (e % 2).  That is the
+// key order of one lane's half of a 16-key product step, so a kernel whose
+// lanes hold one query row draws once per 16 keys.
+struct DropoutCfg {
+  int enabled;
+  uint32_t seed_lo, seed_hi;
+  int t16;          // keep iff draw >= t16 (0 .. 65536)
+  float scale;      // 1 / (1 - p)
+};
+
+// Draws for keys 16 G + 4 s + {0..3, 8..11} of one row (one call).
+__device__ inline u32x4 dropout_draws(const DropoutCfg& d, int G, int s, int row, int head,
+                                      int batch) {
+  return philox4x32_10(u32x4{(uint32_t)(2 * G + s), (uint32_t)row, (uint32_t)head, (uint32_t)batch},
+                       d.seed_lo, d.seed_hi);
+}
+
+// Half e (0..7) of a call's draws, as the multiplier of the probability.
+__device__ inline float dropout_factor(const DropoutCfg& d, u32x4 r, int e) {
+  const uint32_t w = r[e >> 1];
+  const int v = (int)((e & 1) ? (w >> 16) : (w & 0xffffu));
+  return v >= d.t16 ? d.scale : 0.f;
+}
+
+// The multiplier of one element (one call per element).
+__device__ inline float dropout_factor_at(const DropoutCfg& d, int row, int key, int head,
+                                          int batch) {
+  const int w = key & 15;
+  const u32x4 r = dropout_draws(d, key >> 4, (w >> 2) & 1, row, head, batch);
+  return dropout_factor(d, r, (w & 3) | ((w >> 3) << 2));
+}
+
 }  // namespace fa

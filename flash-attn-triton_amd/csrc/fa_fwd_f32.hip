@@ -265,6 +265,15 @@ void fwd_f32_kernel(const FwdParams p) {
       pv[v] = exp2f(fmaf(s[v], sl, -m_use));
       l_run += pv[v];
     }
+    if (MODE == kModePrefill && GENERIC && p.drop.enabled) {
+      // The row sum above is of the undropped P; the product takes the dropped one.
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        const u32x4 r = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pv[8 * cc + e] *= dropout_factor(p.drop, r, e);
+      }
+    }
 
     // O^T += V^T P^T.
 #pragma unroll

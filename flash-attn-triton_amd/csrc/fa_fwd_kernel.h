@@ -72,6 +72,8 @@ struct FwdParams {
   int num_splits, split_tiles;
   float* o_part; float* lse_part;
   int n_mblocks, total_blocks, heavy_first;
+  // Dropout of the probabilities (prefill, GENERIC instantiations only).
+  DropoutCfg drop;
 };
 
 template <int D, int NW, int BN>
@@ -409,10 +411,19 @@ void fwd_kernel(const FwdParams p) {
         const f32x16& sv = s[cc >> 1];
         const int o8 = (cc & 1) * 8;
         u32x4 pb;
-        pb[0] = T::pack2(sv[o8 + 0], sv[o8 + 1]);
-        pb[1] = T::pack2(sv[o8 + 2], sv[o8 + 3]);
-        pb[2] = T::pack2(sv[o8 + 4], sv[o8 + 5]);
-        pb[3] = T::pack2(sv[o8 + 6], sv[o8 + 7]);
+        if (MODE == kModePrefill && GENERIC && p.drop.enabled) {
+          // Row sums above use the undropped P; the product takes the dropped one.
+          const u32x4 r = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, head, b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            pb[j] = T::pack2(sv[o8 + 2 * j] * dropout_factor(p.drop, r, 2 * j),
+                             sv[o8 + 2 * j + 1] * dropout_factor(p.drop, r, 2 * j + 1));
+        } else {
+          pb[0] = T::pack2(sv[o8 + 0], sv[o8 + 1]);
+          pb[1] = T::pack2(sv[o8 + 2], sv[o8 + 3]);
+          pb[2] = T::pack2(sv[o8 + 4], sv[o8 + 5]);
+          pb[3] = T::pack2(sv[o8 + 6], sv[o8 + 7]);
+        }
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
           const uint16_t* vrow = Vt + (db * 32 + c32) * VSTR + cc * 16 + g * 4;

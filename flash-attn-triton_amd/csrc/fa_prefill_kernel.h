@@ -350,6 +350,26 @@ void prefill_kernel(const FwdParams p) {
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float lq[4] = {0.f, 0.f, 0.f, 0.f};   // independent partial row sums
+    if (GENERIC && p.drop.enabled) {
+      // Dropout: the row sums take the undropped P, the product the dropped
+      // one (one Philox call per 16 keys of this lane's row).
+#pragma unroll
+      for (int cc = 0; cc < NCC; ++cc) {
+        const f32x16& sv = sc[cc >> 1];
+        const int o8 = (cc & 1) * 8;
+        const u32x4 r = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
+          const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
+          lq[j] += e0 + e1;
+          pb[cc][j] = T::pack2(e0 * dropout_factor(p.drop, r, 2 * j),
+                               e1 * dropout_factor(p.drop, r, 2 * j + 1));
+        }
+      }
+      l_run += (lq[0] + lq[1]) + (lq[2] + lq[3]);
+      return;
+    }
 #pragma unroll
     for (int cc = 0; cc < NCC; ++cc) {
       const f32x16& sv = sc[cc >> 1];

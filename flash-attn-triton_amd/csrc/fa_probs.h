@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fa_common.h"
+
 namespace fa {
 
 struct ProbsParams {
@@ -18,6 +20,7 @@ struct ProbsParams {
   const float* alibi; int64_t alibi_sb;
   const float* bias; int64_t bias_sb, bias_sh, bias_sq, bias_sk;
   int causal, q_offset, window_left, window_right;
+  DropoutCfg drop;   // probabilities are returned after dropout, as the forward used them
 };
 
 }  // namespace fa

@@ -96,6 +96,7 @@ __global__ __launch_bounds__(256) void probs_kernel(const ProbsParams p) {
     if (p.window_left >= 0) keep = keep && j >= qpos - p.window_left;
     if (p.window_right >= 0) keep = keep && j <= qpos + p.window_right;
     if (keep) prob = expf(x - lse);
+    if (p.drop.enabled) prob *= dropout_factor_at(p.drop, i, j, h, b);
   }
   p.probs[(((int64_t)b * p.heads_q + h) * p.max_q + i) * p.max_k + j] = prob;
   if (p.lse_out != nullptr && j == 0)

@@ -30,6 +30,7 @@ FA_DTYPE_BF16 = 1
 FA_DTYPE_F32 = 2
 
 _i64 = ctypes.c_int64
+_u64 = ctypes.c_uint64
 _i32 = ctypes.c_int32
 _int = ctypes.c_int
 _f32 = ctypes.c_float
@@ -43,21 +44,22 @@ _SIGNATURES = {
     "fa_last_error_string": (ctypes.c_char_p, []),
     "fa_fwd_dense": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64,
-                            _i64, _f32, _vp, _i64, _vp, _i64p, _vp]),
+                            _i64, _f32, _vp, _i64, _vp, _i64p, _f32, _u64, _vp]),
     "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
-                             _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _vp]),
+                             _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _u64,
+                             _vp]),
     "fa_bwd_dense": (_int, [_vp] * 10 + [_i64] * 6 + [_i64p] * 9 +
-                     [_int, _f32, _int, _i64, _i64, _i64, _f32, _vp, _i64, _vp]),
+                     [_int, _f32, _int, _i64, _i64, _i64, _f32, _vp, _i64, _f32, _u64, _vp]),
     "fa_bwd_varlen": (_int, [_vp] * 12 + [_i64] * 6 + [_i64p] * 9 +
-                      [_int, _f32, _int, _i64, _i64, _f32, _vp, _i64, _vp]),
+                      [_int, _f32, _int, _i64, _i64, _f32, _vp, _i64, _f32, _u64, _vp]),
     "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
     "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                               _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
                               _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp]),
     "fa_attn_probs": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64, _i64,
-                             _f32, _vp, _i64, _vp, _i64p, _vp]),
+                             _f32, _vp, _i64, _vp, _i64p, _f32, _u64, _vp]),
     "fa_kvcache_append": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _i64, _vp,
                                  _i64, _vp, _vp, _i64, _i64, _int, _i64, _i64, _i64, _i64,
                                  _i64p, _i64p, _i64p, _i64p, _int, _vp]),
@@ -127,7 +129,8 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offset: int,
-              window_left: int, window_right: int, softcap: float, alibi, bias=None) -> None:
+              window_left: int, window_right: int, softcap: float, alibi, bias=None,
+              dropout_p: float = 0.0, dropout_seed: int = 0) -> None:
     """q [B,Sq,Hq,D], k/v [B,Sk,Hk,D] (BSHD strides), out like q; lse [B,Hq,Sq] or None;
     bias None or fp32 [B,Hq,Sq,Sk] (any strides, 0 broadcasts)."""
     lib = load()
@@ -141,13 +144,13 @@ def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offse
         _strides(out.stride()[:3]), lse_stride, dtype_code(q.dtype), float(softmax_scale),
         int(bool(causal)), int(q_pos_offset), int(window_left), int(window_right), float(softcap),
         _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)), _ptr(bias), bias_stride,
-        _stream(q.device))
+        float(dropout_p), int(dropout_seed), _stream(q.device))
     _check(status, "fa_fwd_dense")
 
 
 def bwd_dense(q, k, v, out, dout, lse, dq, dk, dv, delta, softmax_scale: float, causal: bool,
               q_pos_offset: int, window_left: int, window_right: int, softcap: float,
-              alibi) -> None:
+              alibi, dropout_p: float = 0.0, dropout_seed: int = 0) -> None:
     """Gradients of fwd_dense: all tensors BSHD ([B,S,H,D]); lse / delta fp32
     [B,Hq,Sq]; dq/dk/dv are written.  See fa_bwd_dense."""
     lib = load()
@@ -159,13 +162,15 @@ def bwd_dense(q, k, v, out, dout, lse, dq, dk, dv, delta, softmax_scale: float, 
         _ptr(dv), _ptr(delta), B, Sq, Sk, Hq, Hk, D, *st, _strides(lse.stride()),
         dtype_code(q.dtype), float(softmax_scale), int(bool(causal)), int(q_pos_offset),
         int(window_left), int(window_right), float(softcap), _ptr(alibi),
-        0 if alibi is None else int(alibi.stride(0)), _stream(q.device))
+        0 if alibi is None else int(alibi.stride(0)), float(dropout_p), int(dropout_seed),
+        _stream(q.device))
     _check(status, "fa_bwd_dense")
 
 
 def bwd_varlen(q, k, v, out, dout, lse, dq, dk, dv, delta, cu_q, cu_k, max_seqlen_q: int,
                max_seqlen_k: int, softmax_scale: float, causal: bool, window_left: int,
-               window_right: int, softcap: float, alibi) -> None:
+               window_right: int, softcap: float, alibi, dropout_p: float = 0.0,
+               dropout_seed: int = 0) -> None:
     """Gradients of fwd_varlen: packed [T,H,D] tensors, lse / delta fp32 [Tq,Hq],
     cu_* int32 [batch+1].  See fa_bwd_varlen."""
     lib = load()
@@ -178,13 +183,14 @@ def bwd_varlen(q, k, v, out, dout, lse, dq, dk, dv, delta, cu_q, cu_k, max_seqle
         int(max_seqlen_k), Hq, Hk, D, *st, _strides(lse.stride()), dtype_code(q.dtype),
         float(softmax_scale), int(bool(causal)), int(window_left), int(window_right),
         float(softcap), _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)),
-        _stream(q.device))
+        float(dropout_p), int(dropout_seed), _stream(q.device))
     _check(status, "fa_bwd_varlen")
 
 
 def attn_probs(q, k, lse, probs, lse_out, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
                softmax_scale: float, causal: bool, q_pos_offset: int, window_left: int,
-               window_right: int, softcap: float, alibi, bias=None) -> None:
+               window_right: int, softcap: float, alibi, bias=None, dropout_p: float = 0.0,
+               dropout_seed: int = 0) -> None:
     """probs fp32 [B,Hq,max_q,max_k] contiguous from q/k and the forward LSE.
 
     Dense (cu_q None): q [B,Sq,Hq,D], k [B,Sk,Hk,D], lse [B,Hq,Sq].  Varlen: q
@@ -210,14 +216,14 @@ def attn_probs(q, k, lse, probs, lse_out, cu_q, cu_k, max_seqlen_q: int, max_seq
         _strides(lse_stride), dtype_code(q.dtype), float(softmax_scale), int(bool(causal)),
         int(q_pos_offset), int(window_left), int(window_right), float(softcap), _ptr(alibi),
         0 if alibi is None else int(alibi.stride(0)), _ptr(bias), bias_stride,
-        _stream(q.device))
+        float(dropout_p), int(dropout_seed), _stream(q.device))
     _check(status, "fa_attn_probs")
 
 
 def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
                softmax_scale: float, causal: bool, window_left: int, window_right: int,
                softcap: float, alibi, seqused_q=None, seqused_k=None, cu_out=None,
-               block_table=None) -> None:
+               block_table=None, dropout_p: float = 0.0, dropout_seed: int = 0) -> None:
     """q [Tq,Hq,D], k/v [Tk,Hk,D] (or paged [pages,page,Hk,D] with block_table);
     cu_* int32 [batch+1]; lse [Tout,Hq] or None; see fa_fwd_varlen."""
     lib = load()
@@ -235,7 +241,7 @@ def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: i
         int(window_left), int(window_right), float(softcap), _ptr(alibi),
         0 if alibi is None else int(alibi.stride(0)), _ptr(seqused_q), _ptr(seqused_k),
         _ptr(cu_out), _ptr(block_table), int(block_table.stride(0)) if paged else 0,
-        int(k.shape[1]) if paged else 0, _stream(q.device))
+        int(k.shape[1]) if paged else 0, float(dropout_p), int(dropout_seed), _stream(q.device))
     _check(status, "fa_fwd_varlen")
 
 

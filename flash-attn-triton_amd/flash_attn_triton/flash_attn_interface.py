@@ -22,7 +22,12 @@ defect or a host-side copy, never changes a correct result):
   varlen calls (deterministic: grouped KV heads are reduced in the kernel,
   not with atomics); fp32 inputs, ``attn_bias``, seqused / paged varlen and
   the KV-cache path are forward only (``backward`` raises
-  ``NotImplementedError``), and ``dropout_p > 0`` is rejected.
+  ``NotImplementedError``);
+* dropout draws its mask from a counter-based Philox4x32-10 generator keyed
+  by a seed from torch's default CPU generator, one independent mask per
+  (batch, head) (the reference's ``tl.rand`` offsets repeat the same mask for
+  every head), and the backward uses the exact gradient of the dropped
+  forward.
 """
 from __future__ import annotations
 
@@ -33,13 +38,13 @@ from typing import Optional
 import torch
 
 from .triton_kernel.attention_kernel import (
-    DROPOUT_MSG,
     _kernel_ready,
     _wrap_grad,
     attention,
     attention_varlen,
     dense_attention,
     dense_forward,
+    new_dropout_seed,
     varlen_attention,
     varlen_forward,
 )
@@ -92,10 +97,10 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     lse [B,Hq,Sq] fp32, probs [B,Hq,Sq,Sk] fp32)`` with -inf LSE and zero
     probabilities for rows that see no key.  ``out`` and ``lse`` come from the
     flash kernel (bias applied in its score epilogue), ``probs`` from
-    ``fa_attn_probs``.
+    ``fa_attn_probs``.  With dropout the returned probabilities are the
+    dropped and rescaled ones the output was computed from (:46-48).
     """
-    if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
+    seed = new_dropout_seed() if dropout_p > 0.0 else 0
     batch, q_len, q_heads, head_dim = q.shape
     k_len = k.shape[1]
     if head_dim not in (16, 32, 64, 128, 256):
@@ -110,11 +115,12 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     out, lse = dense_attention(q, k, v, softmax_scale=scale, causal=causal,
                              q_pos_offset=causal_offset, window_left=window_size[0],
                              window_right=window_size[1], softcap=softcap, alibi=alibi,
-                             return_lse=True, bias=bias)
+                             return_lse=True, bias=bias, dropout_p=dropout_p,
+                             dropout_seed=seed)
     probs = torch.empty((batch, q_heads, q_len, k_len), dtype=torch.float32, device=q.device)
     _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse, probs, None, None, None,
                        q_len, k_len, scale, causal, causal_offset, window_size[0],
-                       window_size[1], softcap, alibi, bias)
+                       window_size[1], softcap, alibi, bias, dropout_p, seed)
     return out, lse, probs
 
 
@@ -127,20 +133,20 @@ def _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen
     probs [B,Hq,max_seqlen_q,max_seqlen_k] fp32 (zero padding))``; each
     sequence is upper-left aligned with local positions.
     """
-    if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
+    seed = new_dropout_seed() if dropout_p > 0.0 else 0
     batch = cu_seqlens_q.numel() - 1
     scale = 1.0 / math.sqrt(q.shape[-1]) if softmax_scale is None else softmax_scale
     out, lse_tok = varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                   max_seqlen_k, softmax_scale=scale, causal=causal,
                                   window_left=window_size[0], window_right=window_size[1],
-                                  softcap=softcap, alibi=alibi, return_lse=True)
+                                  softcap=softcap, alibi=alibi, return_lse=True,
+                                  dropout_p=dropout_p, dropout_seed=seed)
     lses = torch.empty((batch, q.shape[1], max_seqlen_q), dtype=torch.float32, device=q.device)
     probs = torch.empty((batch, q.shape[1], max_seqlen_q, max_seqlen_k), dtype=torch.float32,
                         device=q.device)
     _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse_tok, probs, lses, cu_seqlens_q,
                        cu_seqlens_k, max_seqlen_q, max_seqlen_k, scale, causal, 0,
-                       window_size[0], window_size[1], softcap, alibi)
+                       window_size[0], window_size[1], softcap, alibi, None, dropout_p, seed)
     return out, lses, probs
 
 
@@ -154,7 +160,7 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
         q: (batch_size, seqlen, nheads, headdim)
         k: (batch_size, seqlen, nheads_k, headdim)
         v: (batch_size, seqlen, nheads_k, headdim)
-        dropout_p: float. Dropout probability (only 0.0 is built).
+        dropout_p: float. Dropout probability on the attention probabilities.
         softmax_scale: float. Default 1 / sqrt(headdim).
         causal: bool. Upper-left aligned causal mask.
         window_size: (left, right). Sliding window, -1 = unbounded.
@@ -216,13 +222,13 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
     # Equal-length path: unsupported head dims surface as AssertionError, as in
     # the reference's _launch_dense_forward (attention_kernel.py:1063-1064).
     assert head_dim in {16, 32, 64, 128, 256}
-    if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(head_dim)
     return dense_attention(q, k, v, softmax_scale=softmax_scale, causal=causal,
                            window_left=window_size[0], window_right=window_size[1],
-                           softcap=softcap, alibi=alibi_slopes if use_alibi else None)
+                           softcap=softcap, alibi=alibi_slopes if use_alibi else None,
+                           dropout_p=dropout_p,
+                           dropout_seed=new_dropout_seed() if dropout_p > 0.0 else 0)
 
 
 def flash_attn_func_cross(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -270,14 +276,13 @@ def flash_attn_func_cross(q, k, v, dropout_p=0.0, softmax_scale=None, causal=Fal
         return _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size,
                                      softcap, alibi_slopes, attn_bias,
                                      causal_offset=_causal_offset)[0]
-    if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     return dense_attention(q, k, v, softmax_scale=softmax_scale, causal=causal,
                            q_pos_offset=_causal_offset, window_left=window_size[0],
                            window_right=window_size[1], softcap=softcap,
-                           alibi=alibi_slopes if use_alibi else None)
+                           alibi=alibi_slopes if use_alibi else None, dropout_p=dropout_p,
+                           dropout_seed=new_dropout_seed() if dropout_p > 0.0 else 0)
 
 
 def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -664,9 +669,8 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         return _varlen_attention_with_probs(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                             max_seqlen_k, dropout_p, softmax_scale, causal,
                                             window_size, softcap, alibi)
-    if dropout_p > 0.0:
-        chk.fail(NotImplementedError(DROPOUT_MSG))
     values = chk.flush()   # the one host synchronization of this call
+    seed = new_dropout_seed() if dropout_p > 0.0 else 0
     use_alibi = alibi is not None and bool(values[alibi_any])
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
@@ -682,12 +686,14 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                              softcap=softcap, alibi=alibi if use_alibi else None,
                              seqused_q=seqused_q, seqused_k=seqused_k,
                              out_rows=values[out_rows] if out_rows is not None else None,
-                             cu_out=cu_out, block_table=block_table)
+                             cu_out=cu_out, block_table=block_table, dropout_p=dropout_p,
+                             dropout_seed=seed)
         return _wrap_grad(out, q, k, v)
     return varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                             softmax_scale=softmax_scale, causal=causal,
                             window_left=window_size[0], window_right=window_size[1],
-                            softcap=softcap, alibi=alibi if use_alibi else None)
+                            softcap=softcap, alibi=alibi if use_alibi else None,
+                            dropout_p=dropout_p, dropout_seed=seed)
 
 
 def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,

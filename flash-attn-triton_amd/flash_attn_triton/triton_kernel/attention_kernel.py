@@ -15,7 +15,9 @@ backward runs ``fa_bwd_dense`` / ``fa_bwd_varlen`` (the reference's
 ``_attention.backward`` :1185-1198 and ``_attention_varlen.backward``
 :1322-1361), fp16 and bf16.  Not differentiable (backward raises
 ``NotImplementedError``): fp32 inputs, ``attn_bias``, seqused / paged varlen
-and the KV-cache path.  Dropout is not built and is rejected before launch.
+and the KV-cache path.  Dropout (``dropout_p > 0``) drops probabilities with
+the counter-based Philox mask of the kernels; the seed is drawn from torch's
+default CPU generator unless given, and the backward replays the same mask.
 """
 from __future__ import annotations
 
@@ -27,14 +29,18 @@ import torch
 from .. import _native
 
 __all__ = ["attention", "attention_varlen", "dense_forward", "varlen_forward", "dense_attention",
-           "varlen_attention", "dense_backward", "varlen_backward", "FORWARD_ONLY_MSG"]
+           "varlen_attention", "dense_backward", "varlen_backward", "new_dropout_seed",
+           "FORWARD_ONLY_MSG"]
 
 FORWARD_ONLY_MSG = (
     "flash_attn_triton (gfx950 HIP build): this call has no backward (fp32 inputs, "
     "attn_bias, seqused / paged varlen and the KV-cache path are forward only)")
-DROPOUT_MSG = (
-    "flash_attn_triton (gfx950 HIP build): dropout_p > 0 is not implemented; "
-    "call with dropout_p=0.0")
+
+
+def new_dropout_seed() -> int:
+    """A 62-bit dropout seed from torch's default CPU generator (so
+    ``torch.manual_seed`` makes dropout reproducible; no device sync)."""
+    return int(torch.randint(0, 2 ** 62, (1,), dtype=torch.int64).item())
 
 
 class _ForwardOnly(torch.autograd.Function):
@@ -70,7 +76,8 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
 def dense_forward(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: int = 0,
                   window_left: int = -1, window_right: int = -1, softcap: float = 0.0,
                   alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
-                  bias: Optional[torch.Tensor] = None):
+                  bias: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                  dropout_seed: int = 0):
     """Run the dense HIP kernel on ``[B, S, H, D]`` tensors (any BSHD strides).
 
     ``bias`` (optional) is an fp32 ``[B, Hq, Sq, Sk]`` view (broadcast strides
@@ -85,7 +92,7 @@ def dense_forward(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: 
     if alibi is not None:
         alibi = alibi.to(device=q.device, dtype=torch.float32).contiguous()
     _native.fwd_dense(qk, kk, vk, out, lse, softmax_scale, causal, q_pos_offset, window_left,
-                      window_right, softcap, alibi, bias)
+                      window_right, softcap, alibi, bias, dropout_p, dropout_seed)
     return (out, lse) if return_lse else out
 
 
@@ -96,7 +103,8 @@ def varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
                    seqused_q: Optional[torch.Tensor] = None,
                    seqused_k: Optional[torch.Tensor] = None,
                    out_rows: Optional[int] = None, cu_out: Optional[torch.Tensor] = None,
-                   block_table: Optional[torch.Tensor] = None):
+                   block_table: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                   dropout_seed: int = 0):
     """Run the packed varlen HIP kernel on ``[T, H, D]`` tensors.
 
     ``seqused_q``/``seqused_k`` limit each sequence to its first queries /
@@ -117,7 +125,8 @@ def varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
 
     _native.fwd_varlen(qk, kk, vk, out, lse, i32(cu_q), i32(cu_k), max_seqlen_q, max_seqlen_k,
                        softmax_scale, causal, window_left, window_right, softcap, alibi,
-                       i32(seqused_q), i32(seqused_k), i32(cu_out), i32(block_table))
+                       i32(seqused_q), i32(seqused_k), i32(cu_out), i32(block_table),
+                       dropout_p, dropout_seed)
     return (out, lse) if return_lse else out
 
 
@@ -135,7 +144,8 @@ def _f32_alibi(alibi, device):
 
 def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: bool,
                    q_pos_offset: int = 0, window_left: int = -1, window_right: int = -1,
-                   softcap: float = 0.0, alibi: Optional[torch.Tensor] = None):
+                   softcap: float = 0.0, alibi: Optional[torch.Tensor] = None,
+                   dropout_p: float = 0.0, dropout_seed: int = 0):
     """Gradients ``(dq, dk, dv)`` of ``dense_forward`` from ``dout``, given its
     output and LSE (``fa_bwd_dense``).  Head dim 16 runs at 32 with zero padding
     (the extra dims contribute nothing to the scores and get zero gradients)."""
@@ -147,7 +157,8 @@ def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: boo
         grads = dense_backward(*(_pad_head_dim(t, 32) for t in (q, k, v, out, dout)), lse,
                                softmax_scale=softmax_scale, causal=causal,
                                q_pos_offset=q_pos_offset, window_left=window_left,
-                               window_right=window_right, softcap=softcap, alibi=alibi)
+                               window_right=window_right, softcap=softcap, alibi=alibi,
+                               dropout_p=dropout_p, dropout_seed=dropout_seed)
         return tuple(g[..., :16] for g in grads)
     qk, kk, vk, ok, dok = (_kernel_ready(t) for t in (q, k, v, out, dout))
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -156,14 +167,15 @@ def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: boo
     delta = torch.empty_like(lse)
     _native.bwd_dense(qk, kk, vk, ok, dok, lse, dq, dk, dv, delta, softmax_scale, causal,
                       q_pos_offset, window_left, window_right, softcap,
-                      _f32_alibi(alibi, q.device))
+                      _f32_alibi(alibi, q.device), dropout_p, dropout_seed)
     return dq, dk, dv
 
 
 def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int,
                     *, softmax_scale: float, causal: bool, window_left: int = -1,
                     window_right: int = -1, softcap: float = 0.0,
-                    alibi: Optional[torch.Tensor] = None):
+                    alibi: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                    dropout_seed: int = 0):
     """Gradients ``(dq, dk, dv)`` of ``varlen_forward`` (``fa_bwd_varlen``).
     Rows outside every sequence get zero gradients."""
     if q.dtype == torch.float32:
@@ -175,7 +187,8 @@ def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, max_seqlen_q: int, max_
                                 cu_q, cu_k, max_seqlen_q, max_seqlen_k,
                                 softmax_scale=softmax_scale, causal=causal,
                                 window_left=window_left, window_right=window_right,
-                                softcap=softcap, alibi=alibi)
+                                softcap=softcap, alibi=alibi, dropout_p=dropout_p,
+                                dropout_seed=dropout_seed)
         return tuple(g[..., :16] for g in grads)
     qk, kk, vk, ok, dok = (_kernel_ready(t) for t in (q, k, v, out, dout))
     dq = torch.zeros(q.shape, dtype=q.dtype, device=q.device)
@@ -185,7 +198,8 @@ def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, max_seqlen_q: int, max_
     i32 = lambda t: t.to(device=q.device, dtype=torch.int32).contiguous()
     _native.bwd_varlen(qk, kk, vk, ok, dok, lse, dq, dk, dv, delta, i32(cu_q), i32(cu_k),
                        max_seqlen_q, max_seqlen_k, softmax_scale, causal, window_left,
-                       window_right, softcap, _f32_alibi(alibi, q.device))
+                       window_right, softcap, _f32_alibi(alibi, q.device), dropout_p,
+                       dropout_seed)
     return dq, dk, dv
 
 
@@ -194,24 +208,25 @@ class _DenseAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, softmax_scale, causal, q_pos_offset, window_left, window_right,
-                softcap, alibi):
+                softcap, alibi, dropout_p, dropout_seed):
         out, lse = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
                                  q_pos_offset=q_pos_offset, window_left=window_left,
                                  window_right=window_right, softcap=softcap, alibi=alibi,
-                                 return_lse=True)
+                                 return_lse=True, dropout_p=dropout_p, dropout_seed=dropout_seed)
         ctx.save_for_backward(q, k, v, out, lse, alibi)
-        ctx.opts = (softmax_scale, causal, q_pos_offset, window_left, window_right, softcap)
+        ctx.opts = (softmax_scale, causal, q_pos_offset, window_left, window_right, softcap,
+                    dropout_p, dropout_seed)
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, _dlse):
         q, k, v, out, lse, alibi = ctx.saved_tensors
-        scale, causal, off, wl, wr, cap = ctx.opts
+        scale, causal, off, wl, wr, cap, dp, seed = ctx.opts
         dq, dk, dv = dense_backward(q, k, v, out, dout, lse, softmax_scale=scale, causal=causal,
                                     q_pos_offset=off, window_left=wl, window_right=wr,
-                                    softcap=cap, alibi=alibi)
-        return dq, dk, dv, None, None, None, None, None, None, None
+                                    softcap=cap, alibi=alibi, dropout_p=dp, dropout_seed=seed)
+        return (dq, dk, dv) + (None,) * 9
 
 
 class _VarlenAttention(torch.autograd.Function):
@@ -219,58 +234,64 @@ class _VarlenAttention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k, softmax_scale, causal,
-                window_left, window_right, softcap, alibi):
+                window_left, window_right, softcap, alibi, dropout_p, dropout_seed):
         out, lse = varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
                                   softmax_scale=softmax_scale, causal=causal,
                                   window_left=window_left, window_right=window_right,
-                                  softcap=softcap, alibi=alibi, return_lse=True)
+                                  softcap=softcap, alibi=alibi, return_lse=True,
+                                  dropout_p=dropout_p, dropout_seed=dropout_seed)
         ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k, alibi)
         ctx.opts = (max_seqlen_q, max_seqlen_k, softmax_scale, causal, window_left,
-                    window_right, softcap)
+                    window_right, softcap, dropout_p, dropout_seed)
         ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, _dlse):
         q, k, v, out, lse, cu_q, cu_k, alibi = ctx.saved_tensors
-        mq, mk, scale, causal, wl, wr, cap = ctx.opts
+        mq, mk, scale, causal, wl, wr, cap, dp, seed = ctx.opts
         dq, dk, dv = varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, mq, mk,
                                      softmax_scale=scale, causal=causal, window_left=wl,
-                                     window_right=wr, softcap=cap, alibi=alibi)
-        return (dq, dk, dv) + (None,) * 10
+                                     window_right=wr, softcap=cap, alibi=alibi, dropout_p=dp,
+                                     dropout_seed=seed)
+        return (dq, dk, dv) + (None,) * 12
 
 
 def dense_attention(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset: int = 0,
                     window_left: int = -1, window_right: int = -1, softcap: float = 0.0,
                     alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
-                    bias: Optional[torch.Tensor] = None):
+                    bias: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                    dropout_seed: int = 0):
     """``dense_forward`` that is differentiable in q, k, v (fp16 / bf16)."""
     if not _needs_grad(q, k, v) or bias is not None:
         res = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
                             q_pos_offset=q_pos_offset, window_left=window_left,
                             window_right=window_right, softcap=softcap, alibi=alibi,
-                            return_lse=return_lse, bias=bias)
+                            return_lse=return_lse, bias=bias, dropout_p=dropout_p,
+                            dropout_seed=dropout_seed)
         if return_lse:
             return _wrap_grad(res[0], q, k, v), res[1]
         return _wrap_grad(res, q, k, v)
     out, lse = _DenseAttention.apply(q, k, v, softmax_scale, causal, q_pos_offset, window_left,
-                                     window_right, softcap, alibi)
+                                     window_right, softcap, alibi, dropout_p, dropout_seed)
     return (out, lse) if return_lse else out
 
 
 def varlen_attention(q, k, v, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: int, *,
                      softmax_scale: float, causal: bool, window_left: int = -1,
                      window_right: int = -1, softcap: float = 0.0,
-                     alibi: Optional[torch.Tensor] = None, return_lse: bool = False):
+                     alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
+                     dropout_p: float = 0.0, dropout_seed: int = 0):
     """``varlen_forward`` that is differentiable in q, k, v (fp16 / bf16)."""
     if not _needs_grad(q, k, v):
         return varlen_forward(q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
                               softmax_scale=softmax_scale, causal=causal,
                               window_left=window_left, window_right=window_right,
-                              softcap=softcap, alibi=alibi, return_lse=return_lse)
+                              softcap=softcap, alibi=alibi, return_lse=return_lse,
+                              dropout_p=dropout_p, dropout_seed=dropout_seed)
     out, lse = _VarlenAttention.apply(q, k, v, cu_q, cu_k, max_seqlen_q, max_seqlen_k,
                                       softmax_scale, causal, window_left, window_right, softcap,
-                                      alibi)
+                                      alibi, dropout_p, dropout_seed)
     return (out, lse) if return_lse else out
 
 
@@ -299,8 +320,8 @@ def attention(q, k, v, causal=False, sm_scale=None, dropout_p=0.0, dropout_seed=
     head_dim_q, head_dim_k, head_dim_v = q.shape[-1], k.shape[-1], v.shape[-1]
     assert head_dim_q == head_dim_k == head_dim_v
     assert head_dim_k in {16, 32, 64, 128, 256}
-    if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
+    if dropout_seed is None:
+        dropout_seed = new_dropout_seed() if dropout_p > 0.0 else 0
     if alibi_slopes is None:
         use_alibi = False
     elif use_alibi is None:
@@ -315,7 +336,8 @@ def attention(q, k, v, causal=False, sm_scale=None, dropout_p=0.0, dropout_seed=
     out = dense_attention(
         q.transpose(1, 2), k.transpose(1, 2)[:, :seq_len_k], v.transpose(1, 2)[:, :seq_len_k],
         softmax_scale=sm_scale, causal=causal, q_pos_offset=seq_len_k - seq_len_q,
-        window_left=window_left, window_right=window_right, softcap=softcap, alibi=alibi)
+        window_left=window_left, window_right=window_right, softcap=softcap, alibi=alibi,
+        dropout_p=dropout_p, dropout_seed=dropout_seed)
     return out.transpose(1, 2)
 
 
@@ -325,8 +347,8 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     """Packed variable-length forward (reference attention_kernel.py:1364-1380)."""
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(q.shape[-1])
-    if dropout_p > 0.0:
-        raise NotImplementedError(DROPOUT_MSG)
+    if dropout_seed is None:
+        dropout_seed = new_dropout_seed() if dropout_p > 0.0 else 0
     if alibi_slopes is None:
         use_alibi = False
     elif use_alibi is None:
@@ -334,4 +356,5 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seql
     return varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                             softmax_scale=sm_scale, causal=causal, window_left=window_left,
                             window_right=window_right, softcap=softcap,
-                            alibi=alibi_slopes if use_alibi else None)
+                            alibi=alibi_slopes if use_alibi else None, dropout_p=dropout_p,
+                            dropout_seed=dropout_seed)

@@ -63,6 +63,15 @@ const char* fa_last_error_string(void);
  * j*bias_stride[3]] (stride 0 broadcasts).  lse (nullable, fp32) receives the
  * natural-log logsumexp at lse[b*lse_stride[0] + h*lse_stride[1] +
  * i*lse_stride[2]]; rows with no visible key get out = 0 and lse = -inf.
+ *
+ * dropout_p in [0, 1) drops probabilities before the product with V
+ * (attention_kernel.py:344-358): element (b, h, i, j) is kept iff its 16-bit
+ * Philox4x32-10 draw under dropout_seed is >= round(p * 65536), and kept
+ * values are scaled by 1 / (1 - p); the LSE is that of the undropped scores.
+ * The draw of (b, h, i, j) is half j%4 + 4((j%16)/8) of the Philox call with
+ * counter {2(j/16) + (j/4)%2, i, h, b} and key {seed, seed >> 32}; rows and
+ * keys are local to the sequence (varlen: b is the sequence index).  The
+ * backward and fa_attn_probs reproduce the same mask from the same seed.
  */
 int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* lse,
                  int64_t batch, int64_t seqlen_q, int64_t seqlen_k, int64_t heads_q,
@@ -71,7 +80,8 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
                  const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
-                 const int64_t* bias_stride, fa_stream_t stream);
+                 const int64_t* bias_stride, float dropout_p, uint64_t dropout_seed,
+                 fa_stream_t stream);
 
 /* Packed variable-length forward attention.
  *
@@ -106,7 +116,7 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   int64_t alibi_batch_stride, const int32_t* seqused_q,
                   const int32_t* seqused_k, const int32_t* cu_seqlens_out,
                   const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
-                  fa_stream_t stream);
+                  float dropout_p, uint64_t dropout_seed, fa_stream_t stream);
 
 /* Backward of fa_fwd_dense: dq, dk, dv from dout.
  *
@@ -130,7 +140,8 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
                  const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
-                 const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream);
+                 const float* alibi_slopes, int64_t alibi_batch_stride, float dropout_p,
+                 uint64_t dropout_seed, fa_stream_t stream);
 
 /* Backward of fa_fwd_varlen (without seqused / block table).
  *
@@ -148,7 +159,8 @@ int fa_bwd_varlen(const void* q, const void* k, const void* v, const void* out,
                   const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                   int64_t window_left, int64_t window_right, float softcap,
-                  const float* alibi_slopes, int64_t alibi_batch_stride, fa_stream_t stream);
+                  const float* alibi_slopes, int64_t alibi_batch_stride, float dropout_p,
+                  uint64_t dropout_seed, fa_stream_t stream);
 
 /* Split-KV plan for fa_fwd_kvcache: the number of key splits the launch will
  * use and the workspace bytes it needs (0 when num_splits == 1).
@@ -219,7 +231,8 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                   int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
                   const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
-                  const int64_t* bias_stride, fa_stream_t stream);
+                  const int64_t* bias_stride, float dropout_p,
+                  uint64_t dropout_seed, fa_stream_t stream);
 
 /* KV-cache append, the cache write of flash_attn_with_kvcache(k=, v=, ...)
  * (replaces the reference's append at flash_attn_interface.py:468-493, which

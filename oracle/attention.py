@@ -42,7 +42,67 @@ __all__ = [
     "gather_paged_kv",
     "compact_varlen",
     "apply_rotary",
+    "philox4x32_10",
+    "dropout_factors",
 ]
+
+
+# ------------------------------------------------------------------ dropout
+_PHILOX_M0, _PHILOX_M1 = 0xD2511F53, 0xCD9E8D57
+_PHILOX_W0, _PHILOX_W1 = 0x9E3779B9, 0xBB67AE85
+
+
+def philox4x32_10(counter, key) -> np.ndarray:
+    """Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+    easy as 1, 2, 3", SC 2011; the Random123 parameters) on ``counter [..., 4]``
+    uint32 words under ``key = (k0, k1)``; returns ``[..., 4]`` uint32.
+
+    The reference draws its dropout bits with Triton's ``tl.rand`` (Philox,
+    attention_kernel.py:354, :92), which lives in the Triton dependency; this
+    build defines its own mask (below) on the same generator family.
+    """
+    c = np.asarray(counter, dtype=np.uint64) & 0xFFFFFFFF
+    c0, c1, c2, c3 = (c[..., i].copy() for i in range(4))
+    k0, k1 = int(key[0]) & 0xFFFFFFFF, int(key[1]) & 0xFFFFFFFF
+    mask = np.uint64(0xFFFFFFFF)
+    for r in range(10):
+        if r:
+            k0 = (k0 + _PHILOX_W0) & 0xFFFFFFFF
+            k1 = (k1 + _PHILOX_W1) & 0xFFFFFFFF
+        p0 = np.uint64(_PHILOX_M0) * c0
+        p1 = np.uint64(_PHILOX_M1) * c2
+        c0, c1, c2, c3 = (((p1 >> np.uint64(32)) ^ c1 ^ np.uint64(k0)) & mask, p1 & mask,
+                          ((p0 >> np.uint64(32)) ^ c3 ^ np.uint64(k1)) & mask, p0 & mask)
+    return np.stack([c0, c1, c2, c3], axis=-1).astype(np.uint32)
+
+
+def dropout_factors(seed: int, p: float, batch_ids, heads: int, q_len: int,
+                    k_len: int) -> np.ndarray:
+    """Dropout multipliers ``[len(batch_ids), heads, q_len, k_len]``: 0 for a
+    dropped element, ``1 / (1 - p)`` for a kept one.
+
+    Element (b, h, i, j) keeps iff its 16-bit draw >= round(p * 65536).  Its
+    draw is half ``e = j % 4 + 4 ((j % 16) // 8)`` (word e // 2, high half
+    when e is odd) of the Philox call with counter
+    ``(2 (j // 16) + (j // 4) % 2, i, h, b)`` and key
+    ``(seed mod 2^32, seed // 2^32)``.  Same role as the reference's
+    ``tl.rand(seed, offsets) > p`` (attention_kernel.py:344-358, :91-93),
+    with every head drawing its own mask.
+    """
+    p32 = float(np.float32(p))          # the C ABI takes p as an fp32 value
+    t16 = min(65536, max(0, int(round(p32 * 65536.0))))
+    scale = 1.0 / (1.0 - p32)
+    b = np.asarray(batch_ids, dtype=np.int64)[:, None, None, None]
+    h = np.arange(heads, dtype=np.int64)[None, :, None, None]
+    i = np.arange(q_len, dtype=np.int64)[None, None, :, None]
+    j = np.arange(k_len, dtype=np.int64)[None, None, None, :]
+    shape = (b.shape[0], heads, q_len, k_len)
+    ctr = np.stack(np.broadcast_arrays(2 * (j // 16) + (j // 4) % 2, i, h, b), axis=-1)
+    words = philox4x32_10(ctr.reshape(-1, 4), (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))
+    e = np.broadcast_to(j % 4 + 4 * ((j % 16) // 8), shape).reshape(-1)
+    w = words[np.arange(e.size), e // 2].astype(np.int64)
+    draw = np.where(e % 2 == 1, w >> 16, w & 0xFFFF).reshape(shape)
+    return np.where(draw >= t16, scale, 0.0)
 
 
 def _keep_mask(q_len: int, k_len: int, causal: bool, window_size: Sequence[int],
@@ -63,7 +123,8 @@ def _keep_mask(q_len: int, k_len: int, causal: bool, window_size: Sequence[int],
 
 def attention(q, k, v, softmax_scale: Optional[float] = None, causal: bool = False,
               window_size: Sequence[int] = (-1, -1), softcap: float = 0.0,
-              alibi_slopes=None, attn_bias=None, causal_offset: int = 0
+              alibi_slopes=None, attn_bias=None, causal_offset: int = 0,
+              dropout_p: float = 0.0, dropout_seed: int = 0, batch_ids=None
               ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Dense attention with materialized probabilities.
 
@@ -71,6 +132,10 @@ def attention(q, k, v, softmax_scale: Optional[float] = None, causal: bool = Fal
     float64.  ``q [B,Sq,Hq,D]``, ``k,v [B,Sk,Hk,D]``; ``alibi_slopes`` is
     ``(Hq,)`` or ``(B,Hq)``; ``attn_bias`` broadcasts to ``[B,Hq,Sq,Sk]``.
     Returns ``(out [B,Sq,Hq,D], lse [B,Hq,Sq], probs [B,Hq,Sq,Sk])``, all float64.
+    With ``dropout_p > 0`` the probabilities are multiplied by
+    :func:`dropout_factors` (``batch_ids`` name the batch index of each entry,
+    default ``0..B-1``) before the product with V and in the returned
+    ``probs``; the LSE is that of the undropped scores (:43-48).
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -107,13 +172,17 @@ def attention(q, k, v, softmax_scale: Optional[float] = None, causal: bool = Fal
         probs = np.where(denom > 0, ex / np.where(denom > 0, denom, 1.0), 0.0)
         lse = np.where(denom[..., 0] > 0, np.log(np.where(denom[..., 0] > 0, denom[..., 0], 1.0))
                        + finite_max[..., 0], -np.inf)
+    if dropout_p > 0:
+        ids = np.arange(batch) if batch_ids is None else batch_ids
+        probs = probs * dropout_factors(dropout_seed, dropout_p, ids, q_heads, q_len, k_len)
     out = np.matmul(probs, v.transpose(0, 2, 1, 3)).transpose(0, 2, 1, 3)
     return out, lse, probs
 
 
 def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
                        causal: bool = False, window_size: Sequence[int] = (-1, -1),
-                       softcap: float = 0.0, alibi_slopes=None, causal_offset: int = 0
+                       softcap: float = 0.0, alibi_slopes=None, causal_offset: int = 0,
+                       dropout_p: float = 0.0, dropout_seed: int = 0, batch_ids=None
                        ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Exact gradients ``(dq, dk, dv)`` of :func:`attention`'s output against
     ``dout [B,Sq,Hq,D]``, in float64.
@@ -124,7 +193,11 @@ def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
     torch autograd the same way): ``dV = P^T dO``, ``dP = dO V^T``,
     ``delta = rowsum(dO * O)``, ``dS = P (dP - delta) (1 - tanh^2)`` (the last
     factor only with softcap), ``dQ = scale dS K``, ``dK = scale dS^T Q``;
-    grouped KV heads sum the gradients of their query heads.
+    grouped KV heads sum the gradients of their query heads.  With dropout
+    (multipliers F): ``dV = (F P)^T dO`` and ``dS = P (F dP - delta)`` -- the
+    reference's kernels use ``F P (dP - delta)`` (attention_kernel.py:661,
+    :763), which drops the ``- P delta`` term of dropped elements; this is
+    the derivative of the forward above.
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -136,12 +209,21 @@ def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
     out, _, probs = attention(q, k, v, scale, causal, window_size, softcap, alibi_slopes,
                               None, causal_offset)
+    fac = None
+    if dropout_p > 0:
+        ids = np.arange(batch) if batch_ids is None else batch_ids
+        fac = dropout_factors(dropout_seed, dropout_p, ids, q_heads, q_len, k_len)
+        out = np.matmul(probs * fac, np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)
+                        ).transpose(0, 2, 1, 3)
     kr = np.repeat(k, rep, axis=2).transpose(0, 2, 1, 3)     # [B,H,Sk,D]
     vr = np.repeat(v, rep, axis=2).transpose(0, 2, 1, 3)
     qh = q.transpose(0, 2, 1, 3)                              # [B,H,Sq,D]
     doh = dout.transpose(0, 2, 1, 3)
-    dv_h = np.matmul(probs.transpose(0, 1, 3, 2), doh)        # [B,H,Sk,D]
+    pd = probs if fac is None else probs * fac
+    dv_h = np.matmul(pd.transpose(0, 1, 3, 2), doh)           # [B,H,Sk,D]
     dp = np.matmul(doh, vr.transpose(0, 1, 3, 2))             # [B,H,Sq,Sk]
+    if fac is not None:
+        dp = dp * fac
     delta = np.sum(doh * out.transpose(0, 2, 1, 3), axis=-1, keepdims=True)
     ds = probs * (dp - delta)
     if softcap > 0:
@@ -162,8 +244,8 @@ def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
 
 
 def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, causal=False,
-                     window_size=(-1, -1), softcap=0.0, alibi_slopes=None
-                     ) -> Tuple[np.ndarray, np.ndarray]:
+                     window_size=(-1, -1), softcap=0.0, alibi_slopes=None, dropout_p=0.0,
+                     dropout_seed=0) -> Tuple[np.ndarray, np.ndarray]:
     """Packed variable-length attention.
 
     ``q [Tq,Hq,D]``, ``k,v [Tk,Hk,D]``, ``cu_seqlens_*`` int prefix sums.
@@ -195,7 +277,8 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, ca
             continue
         o, l, _ = attention(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke],
                             softmax_scale, causal, window_size, softcap,
-                            None if slopes is None else slopes[b:b + 1])
+                            None if slopes is None else slopes[b:b + 1],
+                            dropout_p=dropout_p, dropout_seed=dropout_seed, batch_ids=[b])
         out[qs:qe] = o[0]
         lse[qs:qe] = l[0].T
     return out, lse
@@ -203,7 +286,8 @@ def attention_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale=None, ca
 
 def attention_varlen_backward(q, k, v, dout, cu_seqlens_q, cu_seqlens_k, softmax_scale=None,
                               causal=False, window_size=(-1, -1), softcap=0.0,
-                              alibi_slopes=None) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+                              alibi_slopes=None, dropout_p=0.0, dropout_seed=0
+                              ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
     """Gradients of :func:`attention_varlen`: :func:`attention_backward` per
     sequence (attention_kernel.py:107-272); rows outside every sequence get
     zero gradients."""
@@ -226,7 +310,8 @@ def attention_varlen_backward(q, k, v, dout, cu_seqlens_q, cu_seqlens_k, softmax
             continue
         g = attention_backward(q[None, qs:qe], k[None, ks:ke], v[None, ks:ke],
                                dout[None, qs:qe], softmax_scale, causal, window_size, softcap,
-                               None if slopes is None else slopes[b:b + 1])
+                               None if slopes is None else slopes[b:b + 1],
+                               dropout_p=dropout_p, dropout_seed=dropout_seed, batch_ids=[b])
         dq[qs:qe], dk[ks:ke], dv[ks:ke] = g[0][0], g[1][0], g[2][0]
     return dq, dk, dv
 

@@ -90,11 +90,12 @@ def test_kvcache_plan_rejects_bad_sizes(lib):
 def test_entry_points_reject_null_pointers_without_a_device(lib):
     st = _native._strides((0, 0, 0))
     status = lib.fa_fwd_dense(None, None, None, None, None, 1, 1, 1, 1, 1, 64, st, st, st, st,
-                              None, 0, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, None)
+                              None, 0, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, 0.0, 0, None)
     assert status == _native.FA_ERR_INVALID
     assert b"null pointer" in lib.fa_last_error_string()
     status = lib.fa_attn_probs(None, None, None, None, None, None, None, 1, 1, 1, 1, 1, 64, st,
-                               st, st, 0, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, None)
+                               st, st, 0, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, 0.0, 0,
+                               None)
     assert status == _native.FA_ERR_INVALID
 
 
@@ -102,10 +103,10 @@ def test_dense_rejects_unsupported_dtype_and_head_dim(lib):
     st = _native._strides((1024, 64, 64))
     one = ctypes.c_void_p(16)   # never dereferenced: validation fails first
     status = lib.fa_fwd_dense(one, one, one, one, None, 1, 1, 1, 1, 1, 64, st, st, st, st,
-                              None, 7, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, None)
+                              None, 7, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, 0.0, 0, None)
     assert status == _native.FA_ERR_UNSUPPORTED
     status = lib.fa_fwd_dense(one, one, one, one, None, 1, 1, 1, 1, 1, 40, st, st, st, st,
-                              None, 0, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, None)
+                              None, 0, 1.0, 0, 0, -1, -1, 0.0, None, 0, None, None, 0.0, 0, None)
     assert status == _native.FA_ERR_UNSUPPORTED
 
 

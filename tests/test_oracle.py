@@ -363,6 +363,76 @@ def test_varlen_backward_is_per_sequence_backward():
     np.testing.assert_allclose(dv[5], 0.0)
 
 
+# ----------------------------------------------------------------- dropout
+def test_philox_known_answers():
+    # Random123 known-answer vectors for philox4x32, 10 rounds.
+    kat = [((0, 0, 0, 0), (0, 0), (0x6627e8d5, 0xe169c58d, 0xbc57ac4c, 0x9b00dbd8)),
+           ((0xffffffff,) * 4, (0xffffffff, 0xffffffff),
+            (0x408f276d, 0x41c83b0e, 0xa20bc7c6, 0x6d5451fd)),
+           ((0x243f6a88, 0x85a308d3, 0x13198a2e, 0x03707344), (0xa4093822, 0x299f31d0),
+            (0xd16cfe09, 0x94fdcceb, 0x5001e420, 0x24126ea1))]
+    for ctr, key, want in kat:
+        got = ora.philox4x32_10(np.array([ctr], dtype=np.uint64), key)[0]
+        assert tuple(int(x) for x in got) == want
+
+
+@pytest.mark.parametrize("p", [0.1, 0.5, 0.9])
+def test_dropout_keep_rate_and_scale(p):
+    f = ora.dropout_factors(1234, p, [0, 1], 4, 256, 256)
+    kept = f > 0
+    n = kept.size
+    # Binomial: the kept fraction lies within 6 standard deviations of 1 - p.
+    assert abs(kept.mean() - (1 - p)) < 6 * math.sqrt(p * (1 - p) / n)
+    np.testing.assert_allclose(f[kept], 1.0 / (1.0 - float(np.float32(p))), rtol=1e-15)
+    # Every (batch, head) draws its own mask: masks of different heads agree
+    # on about p^2 + (1-p)^2 of the elements, not on all of them.
+    agree = (kept[0, 0] == kept[1, 3]).mean()
+    assert abs(agree - (p * p + (1 - p) ** 2)) < 0.01
+
+
+def test_dropout_mask_is_seed_dependent_and_p0_is_identity():
+    a = ora.dropout_factors(1, 0.5, [0], 2, 64, 64)
+    b = ora.dropout_factors(2, 0.5, [0], 2, 64, 64)
+    assert 0.4 < (a == b).mean() < 0.6
+    np.testing.assert_array_equal(ora.dropout_factors(1, 0.0, [0], 2, 64, 64), 1.0)
+    rng = np.random.default_rng(53)
+    q, k, v = (rng.standard_normal((1, 20, 2, 8)) for _ in range(3))
+    np.testing.assert_array_equal(ora.attention(q, k, v)[0],
+                                  ora.attention(q, k, v, dropout_p=0.0, dropout_seed=9)[0])
+
+
+def test_dropout_known_answer_single_key():
+    # Reference tests/test_compare_implementations.py:161-168: q = k = 0,
+    # v = 1, one key: the output is 1 / (1 - p) where kept, 0 where dropped.
+    q = np.zeros((1, 1, 1, 16))
+    v = np.ones((1, 1, 1, 16))
+    seen = set()
+    for seed in range(64):
+        out = ora.attention(q, q, v, dropout_p=0.5, dropout_seed=seed)[0]
+        assert np.all(out == out.flat[0]) and out.flat[0] in (0.0, 2.0)
+        seen.add(float(out.flat[0]))
+    assert seen == {0.0, 2.0}
+
+
+def test_dropout_backward_matches_finite_differences():
+    rng = np.random.default_rng(54)
+    q, k, v = (rng.standard_normal((1, 6, 2, 4)) for _ in range(3))
+    do = rng.standard_normal((1, 6, 2, 4))
+    kw = dict(softmax_scale=0.6, causal=True, softcap=4.0, dropout_p=0.3, dropout_seed=77)
+    grads = ora.attention_backward(q, k, v, do, **kw)
+    f = lambda a, b, c: float(np.sum(ora.attention(a, b, c, **kw)[0] * do))
+    h = 1e-6
+    for idx, x in enumerate((q, k, v)):
+        num = np.zeros_like(x)
+        for pos in np.ndindex(x.shape):
+            args = [q.copy(), k.copy(), v.copy()]
+            args[idx][pos] += h
+            fp = f(*args)
+            args[idx][pos] -= 2 * h
+            num[pos] = (fp - f(*args)) / (2 * h)
+        np.testing.assert_allclose(grads[idx], num, atol=1e-7)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_kvcache_decode_matches_sdpa_bottom_right(causal):
     rng = np.random.default_rng(41)
