@@ -9,7 +9,8 @@ S_q=S_k=4096, D=128 (``flash_attn_func(q, k, v, causal=True)``).  Other
 workloads (``--workload``): ``dense`` (same shape, non-causal),
 ``int8_causal`` / ``int8`` (config 3, ``attention_int8``, quantization
 prepass included), ``decode`` (config 4, paged GQA decode through
-``flash_attn_with_kvcache``) and ``varlen`` (config 5).
+``flash_attn_with_kvcache``), ``varlen`` (config 5) and ``bwd_causal`` /
+``bwd`` (the backward of config 2: dq, dk, dv; 2.5 x the forward's FLOPs).
 
 FLOP convention (reference README.md:226-229): causal 2*B*H*D*S*(S+1),
 non-causal 4*B*H*D*S^2; varlen counts 4*H*D per unmasked (q, k) pair; decode
@@ -84,6 +85,45 @@ def make_dense(torch, causal):
                 metric="attn fwd TFLOP/s (FP16) S=4096 D=128", bound="mfma", peak=PEAK["fp16"],
                 peak_unit="TFLOP/s", config=cfg, cpu=cpu, native="fwd_dense",
                 kernels=KERNELS["dense"], alg_bytes=4 * B * S * H * D * 2)
+
+
+def make_bwd(torch, causal):
+    """Backward of config 2 (dq, dk, dv from dout, given the forward's output and
+    LSE).  FLOPs by the usual convention: 2.5 x the forward's (five products per
+    visible pair)."""
+    from flash_attn_triton.triton_kernel.attention_kernel import dense_backward, dense_forward
+    B, S, H, D = 4, 4096, 32, 128
+    q, k, v, do = (_randn(torch, (B, S, H, D), s, torch.float16, "cuda") for s in (1, 2, 3, 8))
+    scale = 1.0 / math.sqrt(D)
+    out, lse = dense_forward(q, k, v, softmax_scale=scale, causal=causal, return_lse=True)
+    fwd = 2.0 * B * H * D * S * (S + 1) if causal else 4.0 * B * H * D * S * S
+    flops = 2.5 * fwd
+
+    def step():
+        return dense_backward(q, k, v, out, do, lse, softmax_scale=scale, causal=causal)
+
+    def cpu(budget_s):
+        from oracle import attention as ora
+        heads, t0 = 0, time.perf_counter()
+        while heads < B * H and (time.perf_counter() - t0) < budget_s:
+            b, h = divmod(heads, H)
+            qc, kc, vc, dc = (t[b:b + 1, :, h:h + 1].cpu().numpy() for t in (q, k, v, do))
+            ora.attention_backward(qc, kc, vc, dc, scale, causal)
+            heads += 1
+        dt = time.perf_counter() - t0
+        return {"value": flops / (B * H) * heads / dt / 1e12, "unit": "TFLOP/s",
+                "cores": CPU_THREADS, "kind": "port",
+                "sample": f"float64 numpy oracle gradients (oracle/attention.py "
+                          f"attention_backward) on {heads} of {B * H} (batch, head) pairs, "
+                          f"S=4096, D=128, causal={causal}; {dt:.1f} s; {CPU_THREADS} BLAS threads"}
+
+    cfg = {"workload": f"dense_bwd_fp16_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
+           "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
+           "layout": "BSHD contiguous", "flop_convention": "2.5 x forward"}
+    return dict(step=step, work=flops, unit="TFLOP/s", scale=1e12, dtype="fp16",
+                metric="attn bwd TFLOP/s (FP16) S=4096 D=128", bound="mfma", peak=PEAK["fp16"],
+                peak_unit="TFLOP/s", config=cfg, cpu=cpu, native="bwd_dense",
+                kernels=KERNELS["bwd"], alg_bytes=8 * B * S * H * D * 2 + 2 * B * H * S * 4)
 
 
 def make_int8(torch, causal):
@@ -247,8 +287,10 @@ def make_copy(torch):
 # The dominant kernel(s) of each workload as rocprofv3 names them; the first
 # one is launched once per step.
 KERNELS = {
-    "dense_causal": ("fa::prefill_kernel",),
-    "dense": ("fa::prefill_kernel",),
+    "dense_causal": ("fa::prefill_pp_kernel",),
+    "dense": ("fa::prefill_pp_kernel",),
+    "bwd_causal": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
+    "bwd": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
     "int8_causal": ("fa::int8_fwd_kernel",),
     "int8": ("fa::int8_fwd_kernel",),
     "decode": ("fa::decode_kernel", "fa::decode_combine_kernel"),
@@ -259,6 +301,8 @@ KERNELS = {
 WORKLOADS = {
     "dense_causal": lambda torch: make_dense(torch, True),
     "dense": lambda torch: make_dense(torch, False),
+    "bwd_causal": lambda torch: make_bwd(torch, True),
+    "bwd": lambda torch: make_bwd(torch, False),
     "int8_causal": lambda torch: make_int8(torch, True),
     "int8": lambda torch: make_int8(torch, False),
     "decode": make_decode,
@@ -382,8 +426,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; every box in this pipeline has one GPU and "
-              "the attention forward needs no cross-GPU exchange (see DESIGN.md for how it would "
-              "shard). Run with --gpus 1.", file=sys.stderr)
+              "the attention forward needs no cross-GPU exchange (heads and batches shard across "
+              "GPUs without communication). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     # Counter passes run first, as child processes, while this process has not
