@@ -35,6 +35,8 @@
 // of bank conflicts.
 #pragma once
 
+#include <type_traits>
+
 #include "fa_bwd.h"
 #include "fa_common.h"
 
@@ -103,26 +105,48 @@ __device__ inline int64_t row_base(const BwdParams& p, int64_t sb, int64_t ss, i
   return (p.cu_q != nullptr ? (int64_t)start * ss : (int64_t)b * sb) + (int64_t)head * sh;
 }
 
-template <class T, int D, int NW, int BN>
+// Inverse of swz_off: the logical (row, chunk) stored at chunk position pos of
+// 256-byte line `line` (what an LDS-DMA lane writing that position must load).
+template <int D>
+__device__ inline void swz_inverse(int line, int pos, int& r, int& c) {
+  constexpr int CPR = D / 8;
+  if constexpr (CPR >= 16) {
+    r = line / (CPR / 16);
+    const int s = ((r & 3) << 2) | ((r >> 2) & 3);
+    c = (pos ^ s) | ((line % (CPR / 16)) << 4);
+  } else if constexpr (CPR == 8) {
+    const int x = pos ^ (((line & 1) << 2) | ((line >> 1) & 3));
+    r = 2 * line + (x >> 3);
+    c = x & 7;
+  } else {
+    const int x = pos ^ (line & 3);
+    r = 4 * line + (x >> 2);
+    c = x & 3;
+  }
+}
+
+// K and V tiles of BN keys stream through NS LDS stages filled by LDS-DMA
+// buffer loads issued NS - 1 tiles ahead.
+template <class T, int D, int NW, int BN, int NS>
 struct BwdDqTile {
   static constexpr int BM = 32 * NW;
   static constexpr int NT = 64 * NW;
-  static constexpr int TILE = BN * D;                    // elements per K or V tile
-  static constexpr int LDS_BYTES = 2 * 2 * TILE * 2;     // K, V x 2 slots
+  static constexpr int TILEB = BN * D * 2;       // bytes of one K or V stage
+  static constexpr int IPS = TILEB / 1024;       // 1-KiB DMA instructions per K (or V) stage
+  static constexpr int IPW = 2 * IPS / NW;       // per wave: waves [0, NW/2) load K, the rest V
+  static constexpr int LDS_BYTES = NS * 2 * TILEB;
+  static_assert(IPW * NW == 2 * IPS && IPW > 0, "K and V tiles must split evenly over the waves");
 };
 
-template <class T, int D, int NW, int BN, bool GENERIC, int WPE>
+template <class T, int D, int NW, int BN, int NS, bool GENERIC, int WPE>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void bwd_dq_kernel(const BwdParams p) {
-  using Tile = BwdDqTile<T, D, NW, BN>;
-  constexpr int BM = Tile::BM, NT = Tile::NT, TILE = Tile::TILE;
-  constexpr int CPR = D / 8;
-  constexpr int CHUNKS = BN * CPR;
-  constexpr int KPT = (CHUNKS + NT - 1) / NT;
+  using Tile = BwdDqTile<T, D, NW, BN, NS>;
+  constexpr int BM = Tile::BM, TILEB = Tile::TILEB, IPW = Tile::IPW;
   constexpr int NKC = D / 16, NDB = D / 32, NKB = BN / 32, NCC = BN / 16;
-  static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
 
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint8_t* const smem_b = reinterpret_cast<uint8_t*>(smem);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -158,7 +182,6 @@ void bwd_dq_kernel(const BwdParams p) {
   if (GENERIC && p.alibi != nullptr) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
 
   const int wrow0 = row0 + w * 32;
-  const bool wave_active = wrow0 <= row_last;
   const int qpos_w_min = wrow0 + qoff;
   const int qpos_w_max = min(wrow0 + 31, row_last) + qoff;
   const int wl = p.window_left, wr = p.window_right;
@@ -175,6 +198,7 @@ void bwd_dq_kernel(const BwdParams p) {
   if (wl >= 0) k_lo = max(0, row0 + qoff - wl);
   const int t_begin = k_lo / BN;
   const int t_end = k_hi > k_lo ? (k_hi + BN - 1) / BN : t_begin;
+  const int J = t_end - t_begin;
 
   // ------------------------------------------------------------ Q, dO rows; delta
   u32x4 qreg[NKC], doreg[NKC];
@@ -209,53 +233,35 @@ void bwd_dq_kernel(const BwdParams p) {
     if (l != -INFINITY) lse2 = l * kLog2e;
     if (g == 0) p.delta[lse_base + (int64_t)qi * p.lse_ss] = delta;
   }
+  // Retire these loads before the DMA stream starts (the compiler does not
+  // count the DMA instructions).
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
-  // ------------------------------------------------------------ K / V tiles
-  const uint16_t* kg = static_cast<const uint16_t*>(p.k) + row_base(p, p.k_sb, p.k_ss, p.k_sh, b, kvh, ks);
-  const uint16_t* vg = static_cast<const uint16_t*>(p.v) + row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks);
-  const uint32_t k_row_b = (uint32_t)(p.k_ss * 2);
-  const uint32_t v_row_b = (uint32_t)(p.v_ss * 2);
-  uint32_t k_off[KPT], v_off[KPT];
-  int l_off[KPT];
+  // ------------------------------------------------------------ DMA stream
+  // Waves [0, NW/2) copy K tiles, the others V tiles; lane l writes chunk
+  // position l % 16 of line 4 i' + l / 16 (see swz_inverse).
+  const bool load_k = w < NW / 2;
+  const int j0 = (w % (NW / 2)) * IPW;
+  const int64_t x_ss = load_k ? p.k_ss : p.v_ss;
+  const uint16_t* xg = load_k ? static_cast<const uint16_t*>(p.k) + row_base(p, p.k_sb, p.k_ss, p.k_sh, b, kvh, ks)
+                              : static_cast<const uint16_t*>(p.v) + row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks);
+  uint32_t voff[IPW];
 #pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int c = tid + i * NT;
-    k_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * k_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
-    v_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
-    l_off[i] = swz_off<D>(c / CPR, c % CPR);
+  for (int i = 0; i < IPW; ++i) {
+    int r, c;
+    swz_inverse<D>(4 * (j0 + i) + (lane >> 4), lane & 15, r, c);
+    voff[i] = (uint32_t)r * (uint32_t)(x_ss * 2) + (uint32_t)c * 16;
   }
-  u32x4 kreg[KPT], vreg[KPT];
-  auto load_tiles = [&](int t) {
-    const int n0 = t * BN;
-    const auto rk = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
-    const auto rv = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
+  const uint32_t x_lds = lds_address(smem_b) + (load_k ? 0 : NS * TILEB) + j0 * 1024;
+  auto issue = [&](int it) {   // tile t_begin + it into stage it % NS; past J an empty load
+    const bool live = it < J;
+    const int n0 = (t_begin + (live ? it : 0)) * BN;
+    const u32x4 rs = make_rsrc_words(xg + (int64_t)n0 * x_ss, live ? rows_extent(n0, Sk, x_ss, D) : 0u);
+    const uint32_t dst = x_lds + (it % NS) * TILEB;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      kreg[i] = buf_load16(rk, k_off[i], 0);
-      vreg[i] = buf_load16(rv, v_off[i], 0);
-    }
-  };
-  auto k_slot = [&](int i) { return smem + (i & 1) * TILE; };
-  auto v_slot = [&](int i) { return smem + 2 * TILE + (i & 1) * TILE; };
-  auto store_tiles = [&](int slot) {
-#pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int c = tid + i * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) {
-        store16(k_slot(slot) + l_off[i], kreg[i]);
-        store16(v_slot(slot) + l_off[i], vreg[i]);
-      }
-    }
+    for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, voff[i]);
   };
 
-  auto wave_skips = [&](int t) {
-    const int n0 = t * BN, n1 = n0 + BN;
-    bool skip = !wave_active || n0 >= Sk;
-    if (causal) skip = skip || n0 > qpos_w_max;
-    if (wr >= 0) skip = skip || n0 > qpos_w_max + wr;
-    if (wl >= 0) skip = skip || n1 - 1 < qpos_w_min - wl;
-    return skip;
-  };
   auto wave_masks = [&](int t) {
     const int n0 = t * BN, n1 = n0 + BN;
     bool need = n1 > Sk;
@@ -269,67 +275,117 @@ void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
 
-  auto tile_math = [&](int t, int slot, bool masked) {
-    const uint16_t* Ks = k_slot(slot);
-    const uint16_t* Vs = v_slot(slot);
+  // One tile: operands staged ahead of their products (all A operands of a
+  // 32-key block of S^T / dP^T first; the transposed K reads of dQ^T before
+  // the elementwise work, which hides their latency).
+  auto tile_math = [&](int t, int stage, bool masked) {
+    const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem_b + stage * TILEB);
+    const uint16_t* Vs = reinterpret_cast<const uint16_t*>(smem_b + (NS + stage) * TILEB);
+    constexpr bool STAGE = D <= 128;
     f32x16 s[NKB], dp[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
       s[kb] = f32x16{};
       dp[kb] = f32x16{};
+      if constexpr (STAGE) {
+        u32x4 ka[NKC], va[NKC];
 #pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) {
-        const int off = swz_off<D>(kb * 32 + c32, 2 * kc + g);
-        s[kb] = T::mfma32(load16(Ks + off), qreg[kc], s[kb]);
-        dp[kb] = T::mfma32(load16(Vs + off), doreg[kc], dp[kb]);
+        for (int kc = 0; kc < NKC; ++kc) {
+          const int off = swz_off<D>(kb * 32 + c32, 2 * kc + g);
+          ka[kc] = load16(Ks + off);
+          va[kc] = load16(Vs + off);
+        }
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+          s[kb] = T::mfma32(ka[kc], qreg[kc], s[kb]);
+          dp[kb] = T::mfma32(va[kc], doreg[kc], dp[kb]);
+        }
+        // Half the reads up front, then one read behind every product.
+        __builtin_amdgcn_sched_group_barrier(0x100, NKC, 0);   // LDS reads
+#pragma unroll
+        for (int i = 0; i < NKC; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, NKC, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+          const int off = swz_off<D>(kb * 32 + c32, 2 * kc + g);
+          s[kb] = T::mfma32(load16(Ks + off), qreg[kc], s[kb]);
+          dp[kb] = T::mfma32(load16(Vs + off), doreg[kc], dp[kb]);
+        }
       }
+    }
+    constexpr int NTA = STAGE ? NCC * NDB : 1;
+    u32x4 ta[NTA];
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int cc = 0; cc < NCC; ++cc)
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) ta[cc * NDB + db] = tr_operand<D>(Ks, lane, cc, db * 32);
+      __builtin_amdgcn_sched_barrier(0);
     }
     const int n0 = t * BN;
     const bool drop = GENERIC && p.drop.enabled;
     u32x4 dsb[NCC];
+    auto elementwise = [&](auto masked_c) {
+      constexpr bool MASKED = decltype(masked_c)::value;
 #pragma unroll
-    for (int cc = 0; cc < NCC; ++cc) {
-      const int kb = cc >> 1, o8 = (cc & 1) * 8;
-      u32x4 rnd = {0, 0, 0, 0};
-      if (drop) rnd = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
+      for (int cc = 0; cc < NCC; ++cc) {
+        const int kb = cc >> 1, o8 = (cc & 1) * 8;
+        u32x4 rnd = {0, 0, 0, 0};
+        if (drop) rnd = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float ds[2];
+        for (int j = 0; j < 4; ++j) {
+          float ds[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int v = o8 + 2 * j + u;
-          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-          float cg;
-          float pr = bwd_prob<GENERIC>(p, s[kb][v], lse2, slope, qpos, key, cg);
-          if (masked && (key < key_lo || key > key_hi)) pr = 0.f;
-          const float dpv = drop ? dp[kb][v] * dropout_factor(p.drop, rnd, 2 * j + u) : dp[kb][v];
-          ds[u] = pr * (dpv - delta) * cg;
+          for (int u = 0; u < 2; ++u) {
+            const int v = o8 + 2 * j + u;
+            const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
+            float cg;
+            float pr = bwd_prob<GENERIC>(p, s[kb][v], lse2, slope, qpos, key, cg);
+            if (MASKED) pr = (key < key_lo || key > key_hi) ? 0.f : pr;
+            const float dpv = drop ? dp[kb][v] * dropout_factor(p.drop, rnd, 2 * j + u) : dp[kb][v];
+            ds[u] = pr * (dpv - delta) * cg;
+          }
+          dsb[cc][j] = T::pack2(ds[0], ds[1]);
         }
-        dsb[cc][j] = T::pack2(ds[0], ds[1]);
       }
-    }
+    };
+    if (masked)
+      elementwise(std::true_type{});
+    else
+      elementwise(std::false_type{});
 #pragma unroll
     for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
-        acc[db] = T::mfma32(tr_operand<D>(Ks, lane, cc, db * 32), dsb[cc], acc[db]);
+      for (int db = 0; db < NDB; ++db) {
+        if constexpr (STAGE)
+          acc[db] = T::mfma32(ta[cc * NDB + db], dsb[cc], acc[db]);
+        else
+          acc[db] = T::mfma32(tr_operand<D>(Ks, lane, cc, db * 32), dsb[cc], acc[db]);
+      }
     }
   };
 
   // ------------------------------------------------------------ main loop
-  const int J = t_end - t_begin;
-  if (J > 0) {
-    load_tiles(t_begin);
-    store_tiles(0);
-  }
+  // Tiles it .. it + NS - 2 are in flight at the top of iteration it; the
+  // barrier after the wait publishes tile it and retires the reads of tile
+  // it - 1, whose stage the next DMA refills.  The body is straight-line (a
+  // wave whose rows see no key of a tile computes it masked).
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s);
   for (int it = 0; it < J; ++it) {
-    const int t = t_begin + it;
-    __syncthreads();
-    const bool has_next = it + 1 < J;
-    if (has_next) load_tiles(t + 1);
-    if (!wave_skips(t)) tile_math(t, it, wave_masks(t));
-    if (has_next) store_tiles(it + 1);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * IPW));
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + NS - 1);
+    tile_math(t_begin + it, it % NS, wave_masks(t_begin + it));
   }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // ------------------------------------------------------------ dQ = scale * acc
   if (!row_valid) return;
@@ -348,32 +404,38 @@ void bwd_dq_kernel(const BwdParams p) {
   }
 }
 
-template <class T, int D, int NW, int BM>
+// Q and dO tiles of BM rows stream through NS LDS stages, filled by LDS-DMA
+// buffer loads (no VGPR staging) issued NS - 1 tiles ahead; the LSE and delta
+// of the tile's rows ride along (one 4-byte-per-lane DMA each).
+template <class T, int D, int NW, int BM, int NS>
 struct BwdDkvTile {
   static constexpr int BN = 32 * NW;
   static constexpr int NT = 64 * NW;
-  static constexpr int TILE = BM * D;                           // elements per Q or dO tile
-  static constexpr int LDS_BYTES = 2 * 2 * TILE * 2 + 2 * 2 * BM * 4;   // + lse2, delta
+  static constexpr int TILEB = BM * D * 2;       // bytes of one Q or dO stage
+  static constexpr int IPS = TILEB / 1024;       // 1-KiB DMA instructions per Q (or dO) stage
+  static constexpr int IPW = 2 * IPS / NW;       // per wave: waves [0, NW/2) load Q, the rest dO
+  static constexpr int LPS = IPW + 1;            // DMA instructions per wave per stage (+ LSE or delta)
+  static constexpr int FB = 256;                 // bytes of one LSE / delta stage (64 lanes x 4 B)
+  static constexpr int LDS_BYTES = NS * (2 * TILEB + 2 * FB);   // + 4 B per head of the group (ALiBi)
+  static_assert(IPW * NW == 2 * IPS && IPW > 0, "Q and dO tiles must split evenly over the waves");
+  static_assert(BM <= 64 && BM % 32 == 0, "one DMA lane per row for LSE / delta");
 };
 
 // PASS 0 accumulates dK and dV together; at D = 256 the two accumulators do
 // not fit beside K and V, so the launcher runs PASS 1 (dV only) and PASS 2 (dK
 // only), recomputing S in each.
-template <class T, int D, int NW, int BM, bool GENERIC, int WPE, int PASS>
+template <class T, int D, int NW, int BM, int NS, bool GENERIC, int WPE, int PASS>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void bwd_dkdv_kernel(const BwdParams p) {
   constexpr bool DO_DV = PASS != 2, DO_DK = PASS != 1;
-  using Tile = BwdDkvTile<T, D, NW, BM>;
-  constexpr int BN = Tile::BN, NT = Tile::NT, TILE = Tile::TILE;
-  constexpr int CPR = D / 8;
-  constexpr int CHUNKS = BM * CPR;
-  constexpr int KPT = (CHUNKS + NT - 1) / NT;
+  using Tile = BwdDkvTile<T, D, NW, BM, NS>;
+  constexpr int BN = Tile::BN, TILEB = Tile::TILEB, IPW = Tile::IPW, LPS = Tile::LPS;
+  constexpr int FB = Tile::FB;
   constexpr int NKC = D / 16, NDB = D / 32, NRB = BM / 32, NCC = BM / 16;
-  static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
-  static_assert(BM <= NT, "one thread per row stages LSE and delta");
 
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
-  float* fsm = reinterpret_cast<float*>(smem + 4 * TILE);   // [lse2 x2][delta x2]
+  uint8_t* const smem_b = reinterpret_cast<uint8_t*>(smem);
+  float* const slopes_lds = reinterpret_cast<float*>(smem_b + Tile::LDS_BYTES);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -417,6 +479,16 @@ void bwd_dkdv_kernel(const BwdParams p) {
       kreg[kc] = key_valid ? load16(krow + kc * 16 + g * 8) : z;
       vreg[kc] = key_valid && DO_DK ? load16(vrow + kc * 16 + g * 8) : z;
     }
+    // ALiBi slopes of the group's query heads go to LDS now, so that the main
+    // loop issues no vector-memory load besides the DMA stream it counts.
+    if (GENERIC && p.alibi != nullptr) {
+      for (int gi = tid; gi < p.group; gi += NW * 64)
+        slopes_lds[gi] = p.alibi[(int64_t)b * p.alibi_sb + kvh * p.group + gi];
+    }
+    // Retire these loads before the DMA stream starts: the compiler does not
+    // count the DMA instructions and would otherwise wait for all of them at
+    // the first use of kreg.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   }
 
   // Query rows i that see a key of this block: [q_lo, q_hi).
@@ -429,18 +501,9 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const int NM = m_end - m_begin;
   const int J = NM * p.group;
 
-  // This wave's keys [wk0, wk1] and the tiles it may skip or must mask.
+  // This wave's keys [wk0, wk1] and the tiles it must mask.
   const int wk0 = key0 + w * 32;
   const int wk1 = min(wk0 + 31, Sk - 1);
-  const bool wave_active = wk0 < Sk;
-  auto wave_skips = [&](int m0) {
-    const int p0 = m0 + qoff, p1 = m0 + BM - 1 + qoff;
-    bool skip = !wave_active;
-    if (causal) skip = skip || p1 < wk0;
-    if (wr >= 0) skip = skip || p1 + wr < wk0;
-    if (wl >= 0) skip = skip || p0 - wl > wk1;
-    return skip;
-  };
   auto wave_masks = [&](int m0) {
     const int p0 = m0 + qoff, p1 = m0 + BM - 1 + qoff;
     bool need = false;
@@ -449,60 +512,45 @@ void bwd_dkdv_kernel(const BwdParams p) {
     if (wl >= 0) need = need || p1 - wl > wk0;
     return need;
   };
-
-  // ------------------------------------------------------------ Q / dO tiles
-  const uint16_t* qg0 = static_cast<const uint16_t*>(p.q);
-  const uint16_t* dg0 = static_cast<const uint16_t*>(p.dout);
-  const uint32_t q_row_b = (uint32_t)(p.q_ss * 2);
-  const uint32_t d_row_b = (uint32_t)(p.do_ss * 2);
-  uint32_t q_off[KPT], d_off[KPT];
-  int l_off[KPT];
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int c = tid + i * NT;
-    q_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * q_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
-    d_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * d_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
-    l_off[i] = swz_off<D>(c / CPR, c % CPR);
-  }
-  u32x4 qst[KPT], dst[KPT];
-  float lse_st = INFINITY, delta_st = 0.f;
   auto head_of = [&](int it) { return kvh * p.group + it / NM; };
   auto m0_of = [&](int it) { return (m_begin + it % NM) * BM; };
-  auto load_tiles = [&](int it) {
-    const int hq = head_of(it), m0 = m0_of(it);
-    const uint16_t* qg = qg0 + row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hq, qs) + (int64_t)m0 * p.q_ss;
-    const uint16_t* dg = dg0 + row_base(p, p.do_sb, p.do_ss, p.do_sh, b, hq, qs) + (int64_t)m0 * p.do_ss;
-    const auto rq = make_rsrc(qg, rows_extent(m0, Sq, p.q_ss, D));
-    const auto rd = make_rsrc(dg, rows_extent(m0, Sq, p.do_ss, D));
+
+  // ------------------------------------------------------------ DMA stream
+  // Waves [0, NW/2) copy Q tiles, the others dO tiles; each wave writes
+  // IPW consecutive KiB (four 256-byte lines per instruction) of a stage.
+  // Lane l writes chunk position l % 16 of line 4 i' + l / 16 and so loads
+  // the logical (row, chunk) the swizzle puts there.
+  const bool load_q = w < NW / 2;
+  const int j0 = (w % (NW / 2)) * IPW;
+  const int64_t x_ss = load_q ? p.q_ss : p.do_ss;
+  uint32_t voff[IPW];
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      qst[i] = buf_load16(rq, q_off[i], 0);
-      dst[i] = buf_load16(rd, d_off[i], 0);
-    }
-    lse_st = INFINITY;
-    delta_st = 0.f;
-    if (tid < BM && m0 + tid < Sq) {
-      const int64_t li = row_base(p, p.lse_sb, p.lse_ss, p.lse_sh, b, hq, qs) + (int64_t)(m0 + tid) * p.lse_ss;
-      const float l = p.lse[li];
-      if (l != -INFINITY) lse_st = l * kLog2e;
-      delta_st = p.delta[li];
-    }
-  };
-  auto q_slot = [&](int i) { return smem + (i & 1) * TILE; };
-  auto d_slot = [&](int i) { return smem + 2 * TILE + (i & 1) * TILE; };
-  auto store_tiles = [&](int slot) {
+  for (int i = 0; i < IPW; ++i) {
+    int r, c;
+    swz_inverse<D>(4 * (j0 + i) + (lane >> 4), lane & 15, r, c);
+    voff[i] = (uint32_t)r * (uint32_t)(x_ss * 2) + (uint32_t)c * 16;
+  }
+  const uint32_t f_voff = (uint32_t)lane * (uint32_t)(p.lse_ss * 4);
+  const uint32_t x_lds = lds_address(smem_b) + (load_q ? 0 : NS * TILEB) + j0 * 1024;
+  const uint32_t f_lds = lds_address(smem_b) + 2 * NS * TILEB + (w & 1) * NS * FB;
+  auto issue = [&](int it) {   // tile `it` into stage it % NS; past J an empty load
+    const bool live = it < J;
+    const int hq = head_of(live ? it : 0), m0 = m0_of(live ? it : 0);
+    const int stage = it % NS;
+    const uint16_t* src = (load_q ? static_cast<const uint16_t*>(p.q) +
+                                        row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hq, qs)
+                                  : static_cast<const uint16_t*>(p.dout) +
+                                        row_base(p, p.do_sb, p.do_ss, p.do_sh, b, hq, qs)) +
+                          (int64_t)m0 * x_ss;
+    const u32x4 rs = make_rsrc_words(src, live ? rows_extent(m0, Sq, x_ss, D) : 0u);
+    const uint32_t dst = x_lds + stage * TILEB;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) {
-      const int c = tid + i * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) {
-        store16(q_slot(slot) + l_off[i], qst[i]);
-        store16(d_slot(slot) + l_off[i], dst[i]);
-      }
-    }
-    if (tid < BM) {
-      fsm[(slot & 1) * BM + tid] = lse_st;
-      fsm[2 * BM + (slot & 1) * BM + tid] = delta_st;
-    }
+    for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, voff[i]);
+    const float* fsrc = ((w & 1) ? p.delta : p.lse) +
+                        row_base(p, p.lse_sb, p.lse_ss, p.lse_sh, b, hq, qs) + (int64_t)m0 * p.lse_ss;
+    const uint32_t fext =
+        live && m0 < Sq ? (uint32_t)(((int64_t)(Sq - m0 - 1) * p.lse_ss + 1) * 4) : 0u;
+    buf_load4_lds(make_rsrc_words(fsrc, fext), f_lds + stage * FB, f_voff);
   };
 
   f32x16 dk[NDB], dv[NDB];
@@ -512,92 +560,158 @@ void bwd_dkdv_kernel(const BwdParams p) {
     dv[db] = f32x16{};
   }
 
-  auto tile_math = [&](int it, int slot, bool masked) {
-    const uint16_t* Qs = q_slot(slot);
-    const uint16_t* Ds = d_slot(slot);
-    const float* Ls = fsm + (slot & 1) * BM;
-    const float* Es = fsm + 2 * BM + (slot & 1) * BM;
+  // One tile of BM query rows.  The operand reads are staged in registers and
+  // pinned ahead of the products that use them (left to itself the compiler
+  // waits out the LDS latency before every product): all A operands of a
+  // 32-row block of S and dP first, then the products; the transposed Q / dO
+  // reads of the dK / dV products are issued before the elementwise work,
+  // which hides their latency.
+  auto tile_math = [&](int it, int stage, bool masked) {
+    const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem_b + stage * TILEB);
+    const uint16_t* Ds = reinterpret_cast<const uint16_t*>(smem_b + (NS + stage) * TILEB);
+    const float* Ls = reinterpret_cast<const float*>(smem_b + 2 * NS * TILEB + stage * FB);
+    const float* Es = reinterpret_cast<const float*>(smem_b + 2 * NS * TILEB + (NS + stage) * FB);
     const int hq = head_of(it), m0 = m0_of(it);
     float slope = 0.f;
-    if (GENERIC && p.alibi != nullptr) slope = p.alibi[(int64_t)b * p.alibi_sb + hq];
+    if (GENERIC && p.alibi != nullptr) slope = slopes_lds[it / NM];
     f32x16 s[NRB], dp[NRB];
+    // Operands are staged for head dims up to 128; at 256 the staged arrays
+    // would not fit beside the accumulators, so the products read LDS directly.
+    constexpr bool STAGE = D <= 128;
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       s[rb] = f32x16{};
       dp[rb] = f32x16{};
+      if constexpr (STAGE) {
+        u32x4 qa[NKC], da[NKC];
 #pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) {
-        const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
-        s[rb] = T::mfma32(load16(Qs + off), kreg[kc], s[rb]);
-        if (DO_DK) dp[rb] = T::mfma32(load16(Ds + off), vreg[kc], dp[rb]);
+        for (int kc = 0; kc < NKC; ++kc) {
+          const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
+          qa[kc] = load16(Qs + off);
+          if (DO_DK) da[kc] = load16(Ds + off);
+        }
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+          s[rb] = T::mfma32(qa[kc], kreg[kc], s[rb]);
+          if (DO_DK) dp[rb] = T::mfma32(da[kc], vreg[kc], dp[rb]);
+        }
+        constexpr int NR = DO_DK ? 2 * NKC : NKC;
+        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);   // LDS reads
+        __builtin_amdgcn_sched_group_barrier(0x008, NR, 0);   // MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+      } else {
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) {
+          const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
+          s[rb] = T::mfma32(load16(Qs + off), kreg[kc], s[rb]);
+          if (DO_DK) dp[rb] = T::mfma32(load16(Ds + off), vreg[kc], dp[rb]);
+        }
       }
+    }
+    // Transposed operands of dV^T += dO^T P and dK^T += Q^T dS.
+    constexpr int NTA = STAGE ? NCC * NDB : 1;
+    u32x4 ta_v[DO_DV ? NTA : 1], ta_k[DO_DK ? NTA : 1];
+    if constexpr (STAGE) {
+#pragma unroll
+      for (int cc = 0; cc < NCC; ++cc) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          if (DO_DV) ta_v[cc * NDB + db] = tr_operand<D>(Ds, lane, cc, db * 32);
+          if (DO_DK) ta_k[cc * NDB + db] = tr_operand<D>(Qs, lane, cc, db * 32);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     u32x4 pb[NCC], dsb[NCC];
+    auto elementwise = [&](auto masked_c) {
+      constexpr bool MASKED = decltype(masked_c)::value;
 #pragma unroll
-    for (int cc = 0; cc < NCC; ++cc) {
-      const int rb = cc >> 1, o8 = (cc & 1) * 8;
-      // Slots o8 .. o8+7 hold rows 16cc + 4g + {0..3} and 16cc + 8 + 4g + {0..3}.
-      const int r0 = 16 * cc + 4 * g;
-      const f32x4 l0 = *reinterpret_cast<const f32x4*>(Ls + r0);
-      const f32x4 l1 = *reinterpret_cast<const f32x4*>(Ls + r0 + 8);
-      const f32x4 e0 = *reinterpret_cast<const f32x4*>(Es + r0);
-      const f32x4 e1 = *reinterpret_cast<const f32x4*>(Es + r0 + 8);
+      for (int cc = 0; cc < NCC; ++cc) {
+        const int rb = cc >> 1, o8 = (cc & 1) * 8;
+        // Slots o8 .. o8+7 hold rows 16cc + 4g + {0..3} and 16cc + 8 + 4g + {0..3}.
+        const int r0 = 16 * cc + 4 * g;
+        const f32x4 l0 = *reinterpret_cast<const f32x4*>(Ls + r0);
+        const f32x4 l1 = *reinterpret_cast<const f32x4*>(Ls + r0 + 8);
+        const f32x4 e0 = *reinterpret_cast<const f32x4*>(Es + r0);
+        const f32x4 e1 = *reinterpret_cast<const f32x4*>(Es + r0 + 8);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float pv[2], ds[2];
+        for (int j = 0; j < 4; ++j) {
+          float pv[2], ds[2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int v = o8 + 2 * j + u;          // accumulator slot
-          const int rr = 2 * j + u;              // 0..7: rows r0 + rr%4 (+8 for rr >= 4)
-          const float lse2 = rr < 4 ? l0[rr] : l1[rr - 4];
-          const float dl = rr < 4 ? e0[rr] : e1[rr - 4];
-          const int row = m0 + r0 + (rr & 3) + (rr >= 4 ? 8 : 0);
-          const int qpos = row + qoff;
-          float cg;
-          float pr = bwd_prob<GENERIC>(p, s[rb][v], lse2, slope, qpos, kj, cg);
-          if (masked) {
-            bool vis = true;
-            if (causal) vis = vis && kj <= qpos;
-            if (wr >= 0) vis = vis && kj <= qpos + wr;
-            if (wl >= 0) vis = vis && kj >= qpos - wl;
-            if (!vis) pr = 0.f;
+          for (int u = 0; u < 2; ++u) {
+            const int v = o8 + 2 * j + u;          // accumulator slot
+            const int rr = 2 * j + u;              // rows r0 + rr%4 (+8 for rr >= 4)
+            const float lse = rr < 4 ? l0[rr] : l1[rr - 4];
+            const float dl = rr < 4 ? e0[rr] : e1[rr - 4];
+            // Rows with no visible key (LSE -inf) get P = 0; rows past the
+            // sequence read LSE = delta = 0 next to zero Q / dO rows, so they
+            // contribute nothing either.
+            const float lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
+            const int row = m0 + r0 + (rr & 3) + (rr >= 4 ? 8 : 0);
+            const int qpos = row + qoff;
+            float cg;
+            float pr = bwd_prob<GENERIC>(p, s[rb][v], lse2, slope, qpos, kj, cg);
+            if (MASKED) {
+              bool vis = true;
+              if (causal) vis = vis && kj <= qpos;
+              if (wr >= 0) vis = vis && kj <= qpos + wr;
+              if (wl >= 0) vis = vis && kj >= qpos - wl;
+              pr = vis ? pr : 0.f;
+            }
+            float dpv = dp[rb][v];
+            pv[u] = pr;
+            if (GENERIC && p.drop.enabled) {
+              const float f = dropout_factor_at(p.drop, row, kj, hq, b);
+              pv[u] = pr * f;
+              dpv *= f;
+            }
+            ds[u] = pr * (dpv - dl) * cg;
           }
-          float dpv = dp[rb][v];
-          pv[u] = pr;
-          if (GENERIC && p.drop.enabled) {
-            const float f = dropout_factor_at(p.drop, row, kj, hq, b);
-            pv[u] = pr * f;
-            dpv *= f;
-          }
-          ds[u] = pr * (dpv - dl) * cg;
+          pb[cc][j] = T::pack2(pv[0], pv[1]);
+          dsb[cc][j] = T::pack2(ds[0], ds[1]);
         }
-        pb[cc][j] = T::pack2(pv[0], pv[1]);
-        dsb[cc][j] = T::pack2(ds[0], ds[1]);
       }
-    }
+    };
+    if (masked)
+      elementwise(std::true_type{});
+    else
+      elementwise(std::false_type{});
 #pragma unroll
     for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        if (DO_DV) dv[db] = T::mfma32(tr_operand<D>(Ds, lane, cc, db * 32), pb[cc], dv[db]);
-        if (DO_DK) dk[db] = T::mfma32(tr_operand<D>(Qs, lane, cc, db * 32), dsb[cc], dk[db]);
+        if constexpr (STAGE) {
+          if (DO_DV) dv[db] = T::mfma32(ta_v[cc * NDB + db], pb[cc], dv[db]);
+          if (DO_DK) dk[db] = T::mfma32(ta_k[cc * NDB + db], dsb[cc], dk[db]);
+        } else {
+          if (DO_DV) dv[db] = T::mfma32(tr_operand<D>(Ds, lane, cc, db * 32), pb[cc], dv[db]);
+          if (DO_DK) dk[db] = T::mfma32(tr_operand<D>(Qs, lane, cc, db * 32), dsb[cc], dk[db]);
+        }
       }
     }
   };
 
   // ------------------------------------------------------------ main loop
-  if (J > 0) {
-    load_tiles(0);
-    store_tiles(0);
-  }
+  // At the top of iteration it this wave has tiles it .. it + NS - 2 in
+  // flight; once at most NS - 2 tiles remain, tile it has landed, and the
+  // barrier publishes every wave's share of it.  The barrier also retires
+  // the reads of tile it - 1, whose stage the next DMA refills.
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) issue(s);
   for (int it = 0; it < J; ++it) {
-    __syncthreads();
-    const bool has_next = it + 1 < J;
-    if (has_next) load_tiles(it + 1);
-    const int m0 = m0_of(it);
-    if (!wave_skips(m0)) tile_math(it, it, wave_masks(m0));
-    if (has_next) store_tiles(it + 1);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPS));
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    issue(it + NS - 1);
+    // Straight-line body: a tile that holds no visible (row, key) pair for
+    // this wave is computed anyway with the mask (its P is all zero).  A
+    // branch around it would make the dK / dV accumulators a join value that
+    // the compiler copies between register files on every iteration.
+    tile_math(it, it % NS, wave_masks(m0_of(it)));
   }
+  // No DMA may still be writing LDS when the workgroup retires.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // ------------------------------------------------------------ dK = scale * dK^T, dV
   if (!key_valid) return;

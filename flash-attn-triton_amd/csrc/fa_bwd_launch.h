@@ -9,12 +9,12 @@ namespace fa {
 
 // dQ: 4 waves x 32 query rows, 64-key tiles (32 from D = 128, where Q, dO and
 // the dQ^T accumulators take 128 registers; 256 at D = 256).  dK/dV: 4 waves
-// x 32 keys, 64 query rows per tile (32 from D = 128); the dK^T / dV^T
-// accumulators live in the accumulation registers, one wave per SIMD; D = 256
-// accumulates dV and dK in two passes.
+// x 32 keys, 64 query rows per tile (32 from D = 128) in 3 LDS stages; the dK^T
+// / dV^T accumulators live in the accumulation registers, one wave per SIMD;
+// D = 256 accumulates dV and dK in two passes.
 template <int D> struct BwdCfg {
-  static constexpr int DQ_NW = 4, DQ_BN = D >= 128 ? 32 : 64, DQ_WPE = D >= 256 ? 1 : 2;
-  static constexpr int KV_NW = 4, KV_BM = D >= 128 ? 32 : 64, KV_WPE = 1;
+  static constexpr int DQ_NW = 4, DQ_BN = D >= 128 ? 32 : 64, DQ_NS = 3, DQ_WPE = D >= 256 ? 1 : 2;
+  static constexpr int KV_NW = 4, KV_BM = D >= 128 ? 32 : 64, KV_NS = 3, KV_WPE = 1;
 };
 
 template <class Kern>
@@ -29,17 +29,22 @@ hipError_t set_lds(Kern kern, int bytes, bool& done) {
 template <class T, int D, bool GEN, int PASS>
 hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
-  using Tile = BwdDkvTile<T, D, C::KV_NW, C::KV_BM>;
-  auto kern = bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, GEN, C::KV_WPE, PASS>;
+  using Tile = BwdDkvTile<T, D, C::KV_NW, C::KV_BM, C::KV_NS>;
+  auto kern = bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, C::KV_NS, GEN, C::KV_WPE, PASS>;
+  // The ALiBi slope table (one float per query head of the group) follows the
+  // stages; the attribute allows the largest table that still fits.
+  constexpr int kMaxLds = 160 * 1024;
   static bool lds_set = false;
-  hipError_t e = set_lds(kern, Tile::LDS_BYTES, lds_set);
+  hipError_t e = set_lds(kern, kMaxLds, lds_set);
   if (e != hipSuccess) return e;
+  const int64_t lds = Tile::LDS_BYTES + (GEN && p.alibi != nullptr ? 4 * (int64_t)p.group : 0);
+  if (lds > kMaxLds) return hipErrorInvalidConfiguration;
   p.n_blocks = (p.seqlen_k + Tile::BN - 1) / Tile::BN;
   const int64_t total = (int64_t)p.n_blocks * p.heads_k * p.batch;
   if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
   if (total <= 0) return hipSuccess;
   p.total_blocks = (int)total;
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), (unsigned)lds, st, p);
   return hipGetLastError();
 }
 
@@ -47,8 +52,8 @@ template <class T, int D, bool GEN>
 hipError_t launch_bwd_d(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
   {
-    using Tile = BwdDqTile<T, D, C::DQ_NW, C::DQ_BN>;
-    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, GEN, C::DQ_WPE>;
+    using Tile = BwdDqTile<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS>;
+    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS, GEN, C::DQ_WPE>;
     static bool lds_set = false;
     hipError_t e = set_lds(kern, Tile::LDS_BYTES, lds_set);
     if (e != hipSuccess) return e;

@@ -67,35 +67,6 @@ __device__ inline void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Buffer resource as four scalar words (gfx9 raw buffer: base, stride 0,
-// num_records = bytes, word 3 = 32-bit dword format, no swizzle).
-__device__ inline u32x4 make_rsrc_words(const void* base, uint32_t num_bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
-  r[2] = __builtin_amdgcn_readfirstlane(num_bytes);
-  r[3] = 0x00020000u;
-  return r;
-}
-
-// LDS byte address of a pointer into dynamic shared memory.
-__device__ inline uint32_t lds_address(const void* p) {
-  return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) uint8_t*)p);
-}
-
-// Raw buffer load of 16 bytes per lane straight into LDS: lane l's bytes land
-// at LDS address lds + 16 l (lds wave-uniform, through M0).  Written as
-// inline assembly so that the compiler does not treat every later LDS read as
-// dependent on it and wait for all outstanding loads; the kernel waits for
-// these loads itself (s_waitcnt vmcnt) before the barrier that publishes them.
-__device__ inline void buf_load16_lds(const u32x4& r, uint32_t lds, uint32_t voff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-               :
-               : "s"(lds), "v"(voff), "s"(r)
-               : "memory", "m0");
-}
-
 template <class T, int D, bool GENERIC>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_pp_kernel(const FwdParams p) {
