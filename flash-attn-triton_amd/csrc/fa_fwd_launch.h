@@ -99,6 +99,11 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
   }
   const bool masked = p.causal || p.window_left >= 0 || p.window_right >= 0 || p.cu_q != nullptr;
   if constexpr (D == 128) {
+    // The generic epilogue stays on prefill_kernel: measured at BASELINE
+    // config 5 (varlen, causal + window 1024, ALiBi, softcap) the ping-pong
+    // kernel is 1.22x slower there (its 256-row blocks visit every key tile
+    // of the block's window for all rows, and the softmax phase outgrows the
+    // GEMM phase).
     if constexpr (!GEN) return launch_prefill_pp<T, D, GEN>(p, st);
     // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
     // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves.
