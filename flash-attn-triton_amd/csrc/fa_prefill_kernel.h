@@ -296,7 +296,8 @@ void prefill_kernel(const FwdParams p) {
     // GENERIC: scale, ALiBi and softcap, scores -> log2 units.  Otherwise the
     // scores stay raw (scale > 0) and the scale is folded into the exp2
     // argument and the max.
-    if (GENERIC) {
+    // D = 256 keeps the direct form: its registers are already at the limit.
+    if (GENERIC && (BIAS || D >= 256)) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -311,6 +312,57 @@ void prefill_kernel(const FwdParams p) {
             x = p.softcap - 2.f * p.softcap * __builtin_amdgcn_rcpf(1.f + e2);
           }
           sc[kb][v] = x * kLog2e;
+        }
+      }
+    } else if (GENERIC) {
+      // The same transform with its constants folded per tile (this epilogue
+      // is VALU-bound): qpos - key = dq0 - koff with dq0 = qpos - n0 - 4g and
+      // koff = 32 kb + 8 (v / 4) + v % 4 fixed per slot, and with softcap only
+      // x k = x (2 log2 e / softcap) is needed:
+      //   softcap log2(e) tanh(x / softcap) = c2 - 2 c2 / (1 + 2^(x k)),
+      //   x k = s (scale k) - (slope k) |qpos - key|,  c2 = softcap log2(e).
+      const int dq0 = qp32 - n0 - 4 * g;
+      const bool alibi = p.alibi != nullptr;
+      // |qpos - key| as a float: an integer subtract of the slot's offset (an
+      // inline constant below 64) and one convert.
+      auto dist = [&](int kb, int v) { return fabsf((float)(dq0 - (kb * 32 + 8 * (v >> 2) + (v & 3)))); };
+      if (p.softcap > 0.f) {
+        const float sk = p.scale * p.softcap_k, ak = -slope * p.softcap_k;
+        const float c2 = p.softcap * kLog2e, m2c2 = -2.f * c2;
+        auto cap = [&](float xk) {
+          return fmaf(m2c2, __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(xk)), c2);
+        };
+        // (One 32-key block at a time: interleaving the exp / rcp chains of
+        // several blocks buys nothing and costs registers.)
+        if (alibi) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              sc[kb][v] = cap(fmaf(ak, dist(kb, v), sc[kb][v] * sk));
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sc[kb][v] = cap(sc[kb][v] * sk);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      } else {
+        const float sl2 = p.scale * kLog2e, al2 = -slope * kLog2e;
+        if (alibi) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              sc[kb][v] = fmaf(al2, dist(kb, v), sc[kb][v] * sl2);
+        } else {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) sc[kb][v] *= sl2;
         }
       }
     }
