@@ -155,9 +155,9 @@ void bwd_dq_kernel(const BwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
-  int id = xcd_remap(blockIdx.x, p.total_blocks);
-  const int mb = p.n_blocks - 1 - id % p.n_blocks;   // late (longer) rows first
-  id /= p.n_blocks;
+  // Causal: late (longer) rows first.
+  int mb, id;
+  work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, mb, id);
   const int hh = id % p.heads_q;
   const int b = id / p.heads_q;
   const int kvh = hh / p.group;
@@ -444,9 +444,10 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
-  int id = xcd_remap(blockIdx.x, p.total_blocks);
-  const int nb = id % p.n_blocks;
-  id /= p.n_blocks;
+  // Causal: early key blocks (seen by the most rows) first.
+  int nb, id;
+  work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, nb, id);
+  if (p.causal) nb = p.n_blocks - 1 - nb;
   const int kvh = id % p.heads_k;
   const int b = id / p.heads_k;
 

@@ -141,10 +141,8 @@ void int8_fwd_kernel(const Int8Params p) {
   const int c32 = lane & 31;
   const int g = lane >> 5;
 
-  int id = xcd_remap(blockIdx.x, p.total_blocks);
-  int mb = id % p.n_mblocks;
-  const int bh = id / p.n_mblocks;
-  if (p.causal) mb = p.n_mblocks - 1 - mb;
+  int mb, bh;
+  work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.causal != 0, kCausalSpan, mb, bh);
   const int h = bh % p.heads;
   const int b = bh / p.heads;
   const int S = p.seqlen;

@@ -87,12 +87,10 @@ void prefill_kernel(const FwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
-  int id = xcd_remap(blockIdx.x, p.total_blocks);
-  int mb = id % p.n_mblocks;
-  id /= p.n_mblocks;
+  int mb, id;
+  work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.heavy_first != 0, kCausalSpan, mb, id);
   const int hh = id % p.heads_q;
   const int b = id / p.heads_q;
-  if (p.heavy_first) mb = p.n_mblocks - 1 - mb;
   const int kvh = hh / p.group;
 
   int Sq, Sk;
