@@ -67,7 +67,7 @@ __device__ inline void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <class T, int D, bool GENERIC>
+template <class T, int D>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_pp_kernel(const FwdParams p) {
   using Tile = PingPongTile<D>;
@@ -142,8 +142,6 @@ void prefill_pp_kernel(const FwdParams p) {
   const int qpos = qi + qoff32;
   const int qpos_w_min = wrow0 + qoff32;
   const int qpos_w_max = min(wrow0 + 31, row_last) + qoff32;
-  float slope = 0.f;
-  if (GENERIC && p.alibi != nullptr && row_valid) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
 
   const int wl = p.window_left, wr = p.window_right;
   const bool causal = p.causal != 0;
@@ -164,6 +162,12 @@ void prefill_pp_kernel(const FwdParams p) {
   const int J = t_end - t_begin;
 
   // ------------------------------------------------------------ Q^T in VGPRs
+  // fp16: Q is pre-scaled by scale * log2(e) and rounded back to fp16, as the
+  // reference's forward kernel does (attention_kernel.py:492-495), so the
+  // scores come out of the MFMAs in log2 units.  bf16 keeps Q as given (its
+  // 8-bit mantissa would move the log-sum-exp by ~1.5e-3) and scales every
+  // score in the softmax.
+  constexpr bool kPre = std::is_same<T, F16>::value;
   const uint16_t* qg = static_cast<const uint16_t*>(p.q);
   u32x4 qreg[NKC];
   {
@@ -171,6 +175,17 @@ void prefill_pp_kernel(const FwdParams p) {
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc)
       qreg[kc] = row_valid ? load16(qrow + kc * 16 + g * 8) : u32x4{0, 0, 0, 0};
+    if constexpr (kPre) {
+      const float qs = p.scale_log2;
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w2 = qreg[kc][i];
+          qreg[kc][i] = T::pack2(T::to_float((uint16_t)(w2 & 0xffffu)) * qs,
+                                 T::to_float((uint16_t)(w2 >> 16)) * qs);
+        }
+    }
   }
 
   // ------------------------------------------------------------ tile loads
@@ -238,6 +253,13 @@ void prefill_pp_kernel(const FwdParams p) {
   for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
   float m_run = -INFINITY;   // running (possibly stale) max, log2 units
   float l_run = 0.f;         // this lane's partial row sum
+  // m_c: the finite max that P is taken against (m_run, or 0 while the row
+  // has seen no key).  fp16: the S^T products start from -m_c instead of
+  // zero (every lane of cneg holds -m_c of its query row), so they produce
+  // the exponent s - m_c of P directly.
+  float m_c = 0.f;
+  f32x16 cneg = f32x16{};
+  const float sl = kPre ? 1.f : p.scale_log2;
   f32x16 s[NKB];
   u32x4 pbuf[NCC];
 
@@ -289,7 +311,7 @@ void prefill_pp_kernel(const FwdParams p) {
     }
     if constexpr (DO_QK) {
 #pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) s[kb] = f32x16{};
+      for (int kb = 0; kb < NKB; ++kb) s[kb] = kPre ? cneg : f32x16{};
 #pragma unroll
       for (int kc = 0; kc < NKC; ++kc)
 #pragma unroll
@@ -321,27 +343,10 @@ void prefill_pp_kernel(const FwdParams p) {
   };
   using yes = std::true_type;
   using no = std::false_type;
-  // Softmax of the scores in s for the tile starting at key n0: optional
-  // GENERIC transform, boundary mask, lazy max / O rescale, P = exp2(s - m)
-  // packed as the B operand of pv, row sums.
+  // Softmax of the tile starting at key n0 (s: the exponents s - m_c for
+  // fp16, the raw scores for bf16): boundary mask, lazy max / O rescale,
+  // P = exp2(s - m_c) packed as the B operand of pv, row sums.
   auto softmax_tile = [&](int n0, bool masked) {
-    if (GENERIC) {
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-          float x = s[kb][v] * p.scale;
-          if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qpos - key)), x);
-          if (p.softcap > 0.f) {
-            // softcap * tanh(x / softcap) = softcap - 2 softcap / (1 + e^(2x/softcap))
-            const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
-            x = p.softcap - 2.f * p.softcap * __builtin_amdgcn_rcpf(1.f + e2);
-          }
-          s[kb][v] = x * kLog2e;
-        }
-      }
-    }
     if (masked) {
       // Keys outside [key_lo, key_hi] -> -inf, branch-free: the sign of
       // (key_hi - key) | (key - key_lo) selects the -inf bit pattern.
@@ -370,8 +375,8 @@ void prefill_pp_kernel(const FwdParams p) {
           mq[q] = fmaxf(fmaxf(mq[q], s[kb][v + 2 * q]), s[kb][v + 2 * q + 1]);
       }
     }
-    const float sl = GENERIC ? 1.f : p.scale_log2;
-    const float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * sl;
+    const float mq4 = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+    const float mx = kPre ? mq4 + m_c : mq4 * sl;
     const bool raise = mx > m_run + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(raise)) {
       const float m_new = raise ? mx : m_run;
@@ -380,8 +385,18 @@ void prefill_pp_kernel(const FwdParams p) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
       m_run = m_new;
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      if constexpr (kPre) {
+        const float shift = m_use - m_c;   // 0 on the lanes that did not raise
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) s[kb] -= shift;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cneg[v] = -m_use;
+      }
+      m_c = m_use;
     }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    // exp2 argument of score x.
+    auto expo = [&](float x) { return kPre ? x : fmaf(x, sl, -m_c); };
     float lq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int cc = 0; cc < NCC; ++cc) {
@@ -389,8 +404,8 @@ void prefill_pp_kernel(const FwdParams p) {
       const int o8 = (cc & 1) * 8;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
-        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
+        const float e0 = __builtin_amdgcn_exp2f(expo(sv[o8 + 2 * j]));
+        const float e1 = __builtin_amdgcn_exp2f(expo(sv[o8 + 2 * j + 1]));
         pbuf[cc][j] = T::pack2(e0, e1);
         if (T::kSumRounded)
           lq[j] = T::sum2(pbuf[cc][j], lq[j]);
