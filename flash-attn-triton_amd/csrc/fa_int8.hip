@@ -13,23 +13,9 @@
 //
 // The attention kernel follows the schedule of prefill_kernel
 // (fa_prefill_kernel.h); see int8_fwd_kernel below.
-#include "fa_prefill_kernel.h"
+#include "fa_int8_pp.h"
 
 namespace fa {
-
-namespace {
-
-__device__ inline float round_half_away(float x) {
-#pragma clang fp contract(off)
-  return x >= 0.f ? floorf(x + 0.5f) : ceilf(x - 0.5f);
-}
-
-__device__ inline uint32_t pack_i8x4(float a, float b, float c, float d) {
-  return ((uint32_t)(uint8_t)(int8_t)(int)a) | ((uint32_t)(uint8_t)(int8_t)(int)b << 8) |
-         ((uint32_t)(uint8_t)(int8_t)(int)c << 16) | ((uint32_t)(uint8_t)(int8_t)(int)d << 24);
-}
-
-}  // namespace
 
 // One group of D/8 lanes per K row; each lane owns 8 consecutive values.
 // Rows enumerate (b, h, s) of a [B, H, S, D] tensor with arbitrary strides;
@@ -75,17 +61,6 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
   *reinterpret_cast<u32x2*>(k8 + row * D + sub * 8) = out;
   if (sub == 0) s_k[row] = scale;
 }
-
-struct Int8Params {
-  const void* q; const int8_t* k8; const float* s_k; const void* v; void* o; float* lse;
-  int64_t q_sb, q_sh, q_ss;
-  int64_t v_sb, v_sh, v_ss;
-  int64_t o_sb, o_sh, o_ss;
-  int batch, heads, seqlen;
-  float scale_log2;
-  int causal, seq_len_k, seq_len_q;
-  int n_mblocks, total_blocks;
-};
 
 template <int D, int NW, int BN>
 struct Int8Tile {
@@ -412,11 +387,35 @@ hipError_t launch_int8_cfg(Int8Params p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Tile table: causal -> 4 waves, 32-key tiles (less work past the diagonal);
-// otherwise 8 waves sharing 64-key tiles.  D = 256: 8 waves, 32-key tiles.
+// Ping-pong kernel (fa_int8_pp.h): 8 waves, 256 query rows per workgroup.
+template <int D>
+hipError_t launch_int8_pp(Int8Params p, hipStream_t st) {
+  using Tile = Int8PingPongTile<D>;
+  auto kern = int8_pp_kernel<D>;
+  static bool lds_attr_set = false;
+  if (!lds_attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
+    if (e != hipSuccess) return e;
+    lds_attr_set = true;
+  }
+  p.n_mblocks = (p.seqlen + Tile::BM - 1) / Tile::BM;
+  const int64_t total = (int64_t)p.n_mblocks * p.batch * p.heads;
+  if (total <= 0) return hipSuccess;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+  p.total_blocks = (int)total;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  return hipGetLastError();
+}
+
+// Tile table: D = 128 -> the ping-pong kernel.  Otherwise causal -> 4 waves,
+// 32-key tiles (less work past the diagonal), non-causal 8 waves sharing
+// 64-key tiles; D = 256: 8 waves, 32-key tiles.
 template <int D>
 hipError_t launch_int8_fwd(const Int8Params& p, hipStream_t st) {
-  if constexpr (D == 256) {
+  if constexpr (D == 128) {
+    return launch_int8_pp<D>(p, st);
+  } else if constexpr (D == 256) {
     return launch_int8_cfg<D, 8, 32, 2>(p, st);
   } else {
     if (p.causal) return launch_int8_cfg<D, 4, 32, D == 128 ? 3 : 2>(p, st);

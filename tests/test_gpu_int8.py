@@ -73,6 +73,24 @@ def test_int8_attention(causal, head_dim):
     assert np.max(kernel - scheme) <= 2e-3 + 1e-3
 
 
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("lens", [(200, 250), (320, 128), (64, 320), (1, 320)])
+def test_int8_partial_lengths(causal, lens):
+    # seq_len_k masks keys >= seq_len_k (zero-filled past the end of a tile) and
+    # places query row i at i + seq_len_k - seq_len_q; rows before the first
+    # visible key come out as zeros.
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import attention_int8
+    B, H, S, D = 1, 3, 320, 128
+    q = randn((B, H, S, D), 11)
+    k = _outlier_k(B, H, S, D, 12)
+    v = randn((B, H, S, D), 13)
+    out = attention_int8(q.to(DEV), k.to(DEV), v.to(DEV), causal=causal, seq_len_k=lens[0],
+                         seq_len_q=lens[1]).cpu()
+    ref, _ = quant.attention_int8(q.numpy(), k.numpy(), to_np(v), causal=causal,
+                                  seq_len_k=lens[0], seq_len_q=lens[1])
+    assert_close(to_np(out), ref, INT8_ATOL, f"lens={lens}", torch.float16)
+
+
 def test_int8_reference_case():
     # Reference tests/test_compare_implementations.py:222-235 (forward part):
     # B=2, S=128, H=2, D=64, scale 0.125, causal and not.
