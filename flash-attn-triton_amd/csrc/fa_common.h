@@ -157,6 +157,12 @@ __device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t nu
 __device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
+// The same with the non-temporal hint (cache policy NT): for data read once.
+// A plain streaming read measured 7.0 TB/s with it against 6.3 TB/s without
+// on MI355X.
+__device__ inline u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2));
+}
 
 // Byte extent of rows [row0, rows) of a strided 2-byte tensor whose rows hold
 // `row_elems` elements at `row_stride` elements apart, clamped to 32 bits;

@@ -177,7 +177,7 @@ void decode_kernel(const DecodeParams p) {
                               live ? rows_extent(0, L - n0, p.k_ss, D) : 0u);
 #pragma unroll
     for (int m = 0; m < VCH; ++m)
-      kr_[m] = buf_load16(rs, k_voff + (uint32_t)(m * (64 / CPR)) * k_row_b, 0);
+      kr_[m] = buf_load16_nt(rs, k_voff + (uint32_t)(m * (64 / CPR)) * k_row_b, 0);
   };
   u32x4 vreg[VCH];
   auto load_v = [&](int tt) {
@@ -187,7 +187,7 @@ void decode_kernel(const DecodeParams p) {
                               live ? rows_extent(0, L - n0, p.v_ss, D) : 0u);
 #pragma unroll
     for (int m = 0; m < VCH; ++m)
-      vreg[m] = buf_load16(rs, v_voff + (uint32_t)(m * (64 / CPR)) * v_row_b, 0);
+      vreg[m] = buf_load16_nt(rs, v_voff + (uint32_t)(m * (64 / CPR)) * v_row_b, 0);
   };
 
   f32x16 acc[NDB];
