@@ -373,36 +373,41 @@ def measure_traffic(workload, kernels, keep_dir=None):
 
 
 class _LaunchTimer:
-    """Records HIP events on the launch stream around every call of one
-    ``_native`` entry point (the C-ABI launch of the dominant kernel)."""
+    """Records HIP events on the launch stream around every call of one C-ABI
+    entry point (``fa_<name>``, the launch of the dominant kernel).  The
+    events bracket the library call itself, so the Python wrapper's argument
+    preparation, which the GPU would otherwise wait out when its queue is
+    empty (the KV-cache path synchronizes once per call to check its
+    arguments), stays outside the window."""
 
     def __init__(self, torch, name):
         self.torch, self.name, self.pairs = torch, name, []
-        self.orig = None
+        self.orig = self.lib = None
 
     def __enter__(self):
         from flash_attn_triton import _native
         if self.name is None:
             return self
-        self.orig = getattr(_native, self.name)
+        self.lib = _native.load()
+        self.cname = "fa_" + self.name
+        self.orig = getattr(self.lib, self.cname)
         torch, orig, pairs = self.torch, self.orig, self.pairs
 
-        def timed(*a, **kw):
+        def timed(*a):
             stream = torch.cuda.current_stream()
             s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             s.record(stream)
-            r = orig(*a, **kw)
+            r = orig(*a)
             e.record(stream)
             pairs.append((s, e))
             return r
 
-        setattr(_native, self.name, timed)
+        setattr(self.lib, self.cname, timed)
         return self
 
     def __exit__(self, *exc):
         if self.orig is not None:
-            from flash_attn_triton import _native
-            setattr(_native, self.name, self.orig)
+            setattr(self.lib, self.cname, self.orig)
         return False
 
     def mean_s(self):

@@ -85,7 +85,10 @@ void decode_kernel(const DecodeParams p) {
 
   const int L = p.seqlens != nullptr ? p.seqlens[b] : p.max_keys;
   const int k_begin = split * p.split_keys;
-  if (k_begin >= L) return;                    // no keys: the combine skips this split
+  // Splits past the cache end hold no keys (the combine skips them).  Split
+  // 0 always runs, so that an empty cache still writes its rows (0 and LSE
+  // -inf) when there is no combine.
+  if (k_begin >= L && split > 0) return;
   const int k_end = min(L, k_begin + p.split_keys);
 
   const int G = p.group;

@@ -12,6 +12,7 @@ asynchronous on the current stream, as the reference's Triton launches are.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 from pathlib import Path
@@ -245,6 +246,7 @@ def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: i
     _check(status, "fa_fwd_varlen")
 
 
+@functools.lru_cache(maxsize=1024)
 def kvcache_plan(batch: int, seqlen_q: int, heads_q: int, heads_k: int, head_dim: int,
                  max_keys: int, page_size: int = 0):
     lib = load()

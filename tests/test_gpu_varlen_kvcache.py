@@ -105,6 +105,32 @@ def test_paged_kvcache(sq, causal):
     assert_close(to_np(out.cpu()), ref, ATOL[torch.float16], "paged", torch.float16)
 
 
+@pytest.mark.parametrize("lengths", [[0, 50, 0, 3], [0, 3000, 1, 4097, 0, 700], [2049, 0]])
+def test_paged_decode_empty_caches(lengths):
+    # Empty caches give out 0 and LSE -inf on both the one-split path (the
+    # decode kernel writes the final rows) and the split path (the merge
+    # kernel does); repeated calls give the same result.
+    from flash_attn_triton import _native
+    page, hq, hk, d = 256, 8, 2, 128
+    kc, vc, bt = _paged_setup(lengths, page, hk, d, seed=200)
+    q = randn((len(lengths), 1, hq, d), 203)
+    seqlens = torch.tensor(lengths, dtype=torch.int32)
+    ref, ref_lse, _, _ = ora.attention_kvcache(to_np(q), to_np(kc), to_np(vc),
+                                               cache_seqlens=lengths, block_table=bt.numpy())
+    qd, kcd, vcd, btd, sld = (t.to(DEV) for t in (q, kc, vc, bt, seqlens))
+    for rep in range(2):
+        out = torch.full_like(qd, float("nan"))
+        lse = torch.full((len(lengths), hq, 1), float("nan"), device=DEV)
+        _native.fwd_kvcache(qd, kcd, vcd, out, lse, sld, btd, None, None, max(lengths),
+                            1.0 / math.sqrt(d), False, -1, -1, None)
+        torch.cuda.synchronize()
+        assert_close(to_np(out.cpu()), ref, ATOL[torch.float16], f"rep {rep}", torch.float16)
+        got_lse = lse.cpu().numpy()
+        assert np.array_equal(np.isneginf(got_lse), np.isneginf(ref_lse)), f"rep {rep}"
+        fin = np.isfinite(ref_lse)
+        assert np.max(np.abs(got_lse[fin] - ref_lse[fin])) < 1e-3, f"rep {rep}"
+
+
 def test_batched_cache_with_rows_and_leftpad():
     from flash_attn_triton import flash_attn_with_kvcache
     B, cap, hq, hk, d = 3, 300, 4, 4, 64
