@@ -3,31 +3,61 @@
 The reference validates cache lengths, page tables and cu_seqlens with a
 chain of ``torch.any(...)`` / ``.item()`` calls, each of which waits for the
 stream to drain (flash_attn_interface.py:433-470, :583-627).  ``Deferred``
-queues those checks as device flags and reads them all with one
-device-to-host copy.  Exceptions keep the reference's order: a check that
-fails on the host first raises the first failing device check queued before
-it, exactly as the reference's sequential checks would have.
+queues those checks as device scalars and reads them all with one
+device-to-host copy.  Range checks cost one ``aminmax`` launch each, and the
+queued scalars are packed by reinterpreting them as 32-bit words (no
+conversion launches), so a typical decode call validates with three small
+launches.  Exceptions keep the reference's order: a check that fails on the
+host first raises the first failing device check queued before it, exactly
+as the reference's sequential checks would have.
 """
 from __future__ import annotations
 
-from typing import List, Tuple
+import struct
+from typing import List, Optional
 
 import torch
+
+_WORDS = {torch.int32: 1, torch.float32: 1, torch.int64: 2, torch.float64: 2}
+
+
+def _decode(words: List[int], dtype: torch.dtype):
+    if dtype == torch.int32:
+        return words[0]
+    if dtype == torch.int64:
+        return (words[1] << 32) | (words[0] & 0xFFFFFFFF)
+    raw = struct.pack("<" + "i" * len(words), *words)
+    return struct.unpack("<f" if dtype == torch.float32 else "<d", raw)[0]
 
 
 class Deferred:
     def __init__(self) -> None:
-        self._flags: List[Tuple[torch.Tensor, BaseException]] = []
-        self._values: List[torch.Tensor] = []
+        # (kind, exception or None, lo, hi, device scalars); kind "flag": one
+        # boolean, raise if true; "range": (min, max), raise if outside
+        # [lo, hi]; "value": one scalar to return.
+        self._items: list = []
+        self._minmax: dict = {}   # id(tensor) -> (tensor, min, max): one aminmax per tensor
 
     def check(self, bad: torch.Tensor, exc: BaseException) -> None:
         """Queue ``raise exc`` if the device boolean ``bad`` is true."""
-        self._flags.append((bad.reshape(()), exc))
+        self._items.append(("flag", exc, None, None, [bad.reshape(())]))
+
+    def check_range(self, t: torch.Tensor, lo: Optional[int], hi: Optional[int],
+                    exc: BaseException) -> None:
+        """Queue ``raise exc`` unless every element of the integer tensor ``t``
+        lies in ``[lo, hi]`` (``None``: unbounded on that side)."""
+        if t.numel() == 0:
+            return
+        hit = self._minmax.get(id(t))
+        if hit is None or hit[0] is not t:
+            hit = (t, *torch.aminmax(t))
+            self._minmax[id(t)] = hit
+        self._items.append(("range", exc, lo, hi, [hit[1], hit[2]]))
 
     def value(self, t: torch.Tensor) -> int:
         """Queue a device scalar to fetch; returns its index in ``flush()``'s result."""
-        self._values.append(t.reshape(()))
-        return len(self._values) - 1
+        self._items.append(("value", None, None, None, [t.reshape(())]))
+        return sum(1 for it in self._items if it[0] == "value") - 1
 
     def fail(self, exc: BaseException) -> None:
         """A host-side check failed: device checks queued earlier win."""
@@ -36,14 +66,33 @@ class Deferred:
 
     def flush(self) -> list:
         """Raise the first failing queued check; return the queued values."""
-        flags, values = self._flags, self._values
-        self._flags, self._values = [], []
-        if not flags and not values:
+        items, self._items = self._items, []
+        self._minmax = {}
+        if not items:
             return []
-        dev = (flags[0][0] if flags else values[0]).device
-        host = torch.stack([t.to(device=dev, dtype=torch.int64) for t, _ in flags] +
-                           [v.to(device=dev, dtype=torch.int64) for v in values]).tolist()
-        for (_, exc), bad in zip(flags, host):
-            if bad:
+        scalars, dtypes = [], []
+        for it in items:
+            for s in it[4]:
+                s = s.reshape(1)
+                if s.dtype not in _WORDS:
+                    s = s.to(torch.int32 if s.dtype == torch.bool else torch.int64)
+                scalars.append(s.view(torch.int32))
+                dtypes.append(s.dtype)
+        words = (torch.cat(scalars) if len(scalars) > 1 else scalars[0]).tolist()
+        host, pos = [], 0
+        for dt in dtypes:
+            n = _WORDS[dt]
+            host.append(_decode(words[pos:pos + n], dt))
+            pos += n
+        values, k = [], 0
+        for kind, exc, lo, hi, ts in items:
+            got = host[k:k + len(ts)]
+            k += len(ts)
+            if kind == "flag" and got[0]:
                 raise exc
-        return host[len(flags):]
+            if kind == "range" and ((lo is not None and got[0] < lo) or
+                                    (hi is not None and got[1] > hi)):
+                raise exc
+            if kind == "value":
+                values.append(got[0])
+        return values

@@ -353,9 +353,8 @@ def flash_attn_with_kvcache(
             raise ValueError("block_table must have shape (batch, max_num_pages)")
         if block_table.dtype not in (torch.int32, torch.int64):
             raise ValueError("block_table must contain integer page indices")
-        if block_table.numel():
-            chk.check((block_table < 0).any() | (block_table >= k_cache.shape[0]).any(),
-                      ValueError("block_table contains an invalid physical page index"))
+        chk.check_range(block_table, 0, k_cache.shape[0] - 1,
+                        ValueError("block_table contains an invalid physical page index"))
         if cache_leftpad is not None:
             chk.fail(ValueError("cache_leftpad cannot be combined with paged KV caches"))
         page_size = k_cache.shape[1]
@@ -377,8 +376,7 @@ def flash_attn_with_kvcache(
         bad_rows = ValueError("cache_batch_idx must contain valid cache-row indices")
         if cache_rows.numel() != q.shape[0]:
             chk.fail(bad_rows)
-        if cache_rows.numel():
-            chk.check((cache_rows < 0).any() | (cache_rows >= k_cache.shape[0]).any(), bad_rows)
+        chk.check_range(cache_rows, 0, k_cache.shape[0] - 1, bad_rows)
     if cache_leftpad is None:
         leftpads = None
     else:
@@ -386,8 +384,7 @@ def flash_attn_with_kvcache(
         bad_pads = ValueError("cache_leftpad must contain one non-negative value per query batch")
         if leftpads.numel() != q.shape[0]:
             chk.fail(bad_pads)
-        if leftpads.numel():
-            chk.check((leftpads < 0).any(), bad_pads)
+        chk.check_range(leftpads, 0, None, bad_pads)
     zero_pad = 0 if leftpads is None else leftpads
     cos_t = sin_t = None
     if rotary_cos is not None:
@@ -416,22 +413,26 @@ def flash_attn_with_kvcache(
         bad_fit = ValueError("new KV tensors do not fit in the cache")
         if lengths.numel() != q.shape[0]:
             chk.fail(bad_fit)
-        if lengths.numel():
-            chk.check((lengths < 0).any() | (lengths + zero_pad + n_new > cache_capacity).any(),
-                      bad_fit)
+        chk.check_range(lengths, 0, None, bad_fit)
+        chk.check_range(lengths + zero_pad + n_new, None, cache_capacity, bad_fit)
         if cos_t is not None and lengths.numel() and n_new:
             chk.check((lengths + zero_pad + n_new > cos_t.shape[0]).any(), bad_rotary)
     else:
         if cache_seqlens is None:
-            lengths = torch.full((q.shape[0],), cache_capacity, dtype=torch.int64, device=q.device)
+            lengths = torch.full((q.shape[0],), cache_capacity, dtype=torch.int32, device=q.device)
+        elif (isinstance(cache_seqlens, torch.Tensor) and cache_seqlens.device == q.device
+              and cache_seqlens.dtype in (torch.int32, torch.int64)):
+            lengths = cache_seqlens.flatten()   # no conversion launch on the common path
         else:
             lengths = torch.as_tensor(cache_seqlens, device=q.device, dtype=torch.int64).flatten()
         bad_lengths = ValueError("cache_seqlens must contain valid lengths for every batch item")
         if lengths.numel() != q.shape[0]:
             chk.fail(bad_lengths)
-        if lengths.numel():
-            chk.check((lengths < 0).any() | (lengths + zero_pad > cache_capacity).any(),
-                      bad_lengths)
+        if leftpads is None:
+            chk.check_range(lengths, 0, cache_capacity, bad_lengths)
+        else:
+            chk.check_range(lengths, 0, None, bad_lengths)
+            chk.check_range(lengths.long() + leftpads, None, cache_capacity, bad_lengths)
     if cos_t is not None and lengths.numel() and q.shape[1]:
         # Query rows rotate at L + leftpad - Sq + i (L after the append);
         # negative positions index from the end of the tables, as torch
@@ -587,25 +588,31 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         chk.fail(bad_start)
     # With seqused_* the reference re-derives that side's cu_seqlens from the
     # used counts (:563, :581), so its start/order/size checks always pass.
+    # Range checks on cu_seqlens slices and differences: one aminmax launch
+    # per tensor, shared by the checks that read it.
+    cu_q_first, cu_k_first = cu_seqlens_q[:1], cu_seqlens_k[:1]
+    cu_q_last, cu_k_last = cu_seqlens_q[-1:], cu_seqlens_k[-1:]
+    len_q = cu_seqlens_q[1:] - cu_seqlens_q[:-1] if cu_seqlens_q.numel() > 1 else None
+    len_k = cu_seqlens_k[1:] - cu_seqlens_k[:-1] if cu_seqlens_k.numel() > 1 else None
     if seqused_q is None:
-        chk.check(cu_seqlens_q[0] != 0, bad_start)
+        chk.check_range(cu_q_first, 0, 0, bad_start)
     if seqused_k is None:
-        chk.check(cu_seqlens_k[0] != 0, bad_start)
+        chk.check_range(cu_k_first, 0, 0, bad_start)
     if cu_seqlens_q.numel() > 1:
         bad_order = ValueError("cu_seqlens arrays must be monotonically non-decreasing")
         if seqused_q is None:
-            chk.check((cu_seqlens_q[1:] < cu_seqlens_q[:-1]).any(), bad_order)
-        if seqused_k is None:
-            chk.check((cu_seqlens_k[1:] < cu_seqlens_k[:-1]).any(), bad_order)
+            chk.check_range(len_q, 0, None, bad_order)
+        if seqused_k is None and len_k is not None:
+            chk.check_range(len_k, 0, None, bad_order)
     bad_size = ValueError("cu_seqlens values exceed the packed tensor sizes")
     if seqused_q is None:
-        chk.check(cu_seqlens_q[-1] > q.shape[0], bad_size)
+        chk.check_range(cu_q_last, None, q.shape[0], bad_size)
     else:
         chk.check((cu_seqlens_q[:-1] + seqused_q > q.shape[0]).any(), bad_size)
     if paged:
         chk.check(paged_short, bad_size)
     elif seqused_k is None:
-        chk.check(cu_seqlens_k[-1] > k.shape[0], bad_size)
+        chk.check_range(cu_k_last, None, k.shape[0], bad_size)
     else:
         chk.check((cu_seqlens_k[:-1] + seqused_k > k.shape[0]).any(), bad_size)
     kv_heads = k.shape[-2]
@@ -639,18 +646,19 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         # check above passed; seqused_* sides are covered by construction.
         bad_cover = ValueError("cu_seqlens arrays must cover the packed q and KV tensors")
         if seqused_q is None:
-            chk.check(cu_seqlens_q[-1] != q.shape[0], bad_cover)
+            chk.check_range(cu_q_last, q.shape[0], q.shape[0], bad_cover)
         if seqused_k is None:
-            chk.check(cu_seqlens_k[-1] != k.shape[0], bad_cover)
+            chk.check_range(cu_k_last, k.shape[0], k.shape[0], bad_cover)
     elif seqused_q is None:
-        chk.check(cu_seqlens_q[-1] != q.shape[0],
-                  ValueError("cu_seqlens arrays must cover the packed q and KV tensors"))
+        chk.check_range(cu_q_last, q.shape[0], q.shape[0],
+                        ValueError("cu_seqlens arrays must cover the packed q and KV tensors"))
     if cu_seqlens_q.numel() < 2:
         chk.fail(ValueError("cu_seqlens arrays must describe at least one sequence"))
-    used_len_q = seqused_q if seqused_q is not None else cu_seqlens_q[1:] - cu_seqlens_q[:-1]
-    used_len_k = seqused_k if seqused_k is not None else cu_seqlens_k[1:] - cu_seqlens_k[:-1]
-    chk.check((used_len_q.max() > max_seqlen_q) | (used_len_k.max() > max_seqlen_k),
-              ValueError("max sequence lengths must cover every packed sequence"))
+    used_len_q = seqused_q if seqused_q is not None else len_q
+    used_len_k = seqused_k if seqused_k is not None else len_k
+    bad_max = ValueError("max sequence lengths must cover every packed sequence")
+    chk.check_range(used_len_q, None, max_seqlen_q, bad_max)
+    chk.check_range(used_len_k, None, max_seqlen_k, bad_max)
     out_rows = chk.value(seqused_q.sum()) if seqused_q is not None else None
     if max_seqlen_q == 0 or max_seqlen_k == 0:
         values = chk.flush()
