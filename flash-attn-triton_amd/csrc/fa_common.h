@@ -126,9 +126,9 @@ __device__ inline void work_item(int L, int total, int n_mblocks, bool heavy_fir
   if (heavy_first) mb = n_mblocks - 1 - mb;
 }
 
-// work_item span of the causal launches: 4 groups measured best on MI355X for
-// the forward, INT8 and backward kernels at B=4 H=32 S=4096 (1: 5-7% slower,
-// all groups of an XCD: 1-3% slower).
+// work_item span of the causal launches of the ping-pong forward, INT8 and
+// backward kernels: 4 groups measured best on MI355X at B=4 H=32 S=4096 (1:
+// 5-7% slower, all groups of an XCD: 1-3% slower).
 constexpr int kCausalSpan = 4;
 
 __device__ inline u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
