@@ -80,8 +80,9 @@ __device__ inline u32x4 tr_operand(const uint16_t* tile, int lane, int cc, int c
 }
 
 // Per-score transform shared by both kernels: the recomputed probability and
-// the softcap derivative.  `lse2` is the row's LSE in log2 units (+inf for
-// rows that see no key or lie past the sequence, giving P = 0).
+// the softcap derivative.  `lse2` is the row's LSE in log2 units (the dQ
+// kernel passes +inf for a row that sees no key, giving P = 0; the dK/dV
+// kernel passes the row's -inf and masks every pair of such a row).
 template <bool GENERIC>
 __device__ inline float bwd_prob(const BwdParams& p, float s, float lse2, float slope, int qpos,
                                  int key, float& cap_grad) {
@@ -644,10 +645,12 @@ void bwd_dkdv_kernel(const BwdParams p) {
             const int rr = 2 * j + u;              // rows r0 + rr%4 (+8 for rr >= 4)
             const float lse = rr < 4 ? l0[rr] : l1[rr - 4];
             const float dl = rr < 4 ? e0[rr] : e1[rr - 4];
-            // Rows with no visible key (LSE -inf) get P = 0; rows past the
-            // sequence read LSE = delta = 0 next to zero Q / dO rows, so they
-            // contribute nothing either.
-            const float lse2 = lse == -INFINITY ? INFINITY : lse * kLog2e;
+            // Rows with no visible key (LSE -inf, so exp2 gives +inf here)
+            // only occur in tiles that take the mask, which selects P = 0 for
+            // every pair of such a row: an unmasked tile's rows all see every
+            // key of this wave.  Rows past the sequence read LSE = delta = 0
+            // next to zero Q / dO rows and contribute nothing.
+            const float lse2 = lse * kLog2e;
             const int row = m0 + r0 + (rr & 3) + (rr >= 4 ? 8 : 0);
             const int qpos = row + qoff;
             float cg;

@@ -76,6 +76,14 @@ def test_cross_lengths(causal):
 
 
 @pytest.mark.parametrize("d", [64, 128])
+def test_rows_without_visible_keys(d):
+    # Window (8, 8) over 64 keys: query rows past 71 see no key (LSE -inf, zero
+    # output and zero gradient); the dK/dV kernel masks every pair of them.
+    _dense_case(1, 300, 64, 4, 2, d, causal=False, window=(8, 8), seed=23)
+    _dense_case(2, 200, 40, 2, 2, d, causal=True, window=(4, -1), seed=24)
+
+
+@pytest.mark.parametrize("d", [64, 128])
 def test_window_alibi_softcap(d):
     _dense_case(2, 300, 300, 4, 2, d, causal=True, window=(64, 0), softcap=20.0, alibi=True,
                 seed=31)
