@@ -535,10 +535,9 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const uint32_t f_voff = (uint32_t)lane * (uint32_t)(p.lse_ss * 4);
   const uint32_t x_lds = lds_address(smem_b) + (load_q ? 0 : NS * TILEB) + j0 * 1024;
   const uint32_t f_lds = lds_address(smem_b) + 2 * NS * TILEB + (w & 1) * NS * FB;
-  auto issue = [&](int it) {   // tile `it` into stage it % NS; past J an empty load
+  auto issue = [&](int it, int stage) {   // tile `it` into stage it % NS; past J an empty load
     const bool live = it < J;
     const int hq = head_of(live ? it : 0), m0 = m0_of(live ? it : 0);
-    const int stage = it % NS;
     const uint16_t* src = (load_q ? static_cast<const uint16_t*>(p.q) +
                                         row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hq, qs)
                                   : static_cast<const uint16_t*>(p.dout) +
@@ -562,6 +561,40 @@ void bwd_dkdv_kernel(const BwdParams p) {
     dv[db] = f32x16{};
   }
 
+  // Operands are staged for head dims up to 128; at 256 the staged arrays
+  // would not fit beside the accumulators, so the products read LDS directly.
+  constexpr bool STAGE = D <= 128;
+  // Per-lane byte offsets within a stage, computed once (the Q and dO tiles
+  // share them): the row reads of S and dP (row rb*32 + c32, chunk 2 kc + g)
+  // and the two halves of each transposed read of dV and dK (tr_operand's
+  // addressing).  Recomputing the swizzle per tile cost ~90 integer VALU
+  // instructions per tile.
+  uint32_t rd_ofs[STAGE ? NRB * NKC : 1];
+  uint32_t tr_ofs[STAGE ? NCC * NDB * 2 : 1];
+  if constexpr (STAGE) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc)
+        rd_ofs[rb * NKC + kc] = 2u * (uint32_t)swz_off<D>(rb * 32 + c32, 2 * kc + g);
+    const int j = lane & 15;
+#pragma unroll
+    for (int cc = 0; cc < NCC; ++cc)
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) {
+        const int r = 16 * cc + 4 * g + (j >> 2);
+        const int d = db * 32 + 16 * (c32 >> 4) + 4 * (j & 3);
+        tr_ofs[(cc * NDB + db) * 2] = 2u * (uint32_t)(swz_off<D>(r, d >> 3) + (d & 7));
+        tr_ofs[(cc * NDB + db) * 2 + 1] = 2u * (uint32_t)(swz_off<D>(r + 8, d >> 3) + (d & 7));
+      }
+  }
+  auto tr_read = [&](const uint8_t* base, int cc, int db) {
+    const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + tr_ofs[(cc * NDB + db) * 2]));
+    const u32x2 hi =
+        lds_read_tr16(reinterpret_cast<const uint16_t*>(base + tr_ofs[(cc * NDB + db) * 2 + 1]));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+
   // One tile of BM query rows.  The operand reads are staged in registers and
   // pinned ahead of the products that use them (left to itself the compiler
   // waits out the LDS latency before every product): all A operands of a
@@ -577,9 +610,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
     float slope = 0.f;
     if (GENERIC && p.alibi != nullptr) slope = slopes_lds[it / NM];
     f32x16 s[NRB], dp[NRB];
-    // Operands are staged for head dims up to 128; at 256 the staged arrays
-    // would not fit beside the accumulators, so the products read LDS directly.
-    constexpr bool STAGE = D <= 128;
+    const uint8_t* Qb = reinterpret_cast<const uint8_t*>(Qs);
+    const uint8_t* Db = reinterpret_cast<const uint8_t*>(Ds);
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       s[rb] = f32x16{};
@@ -588,9 +620,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
         u32x4 qa[NKC], da[NKC];
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
-          const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
-          qa[kc] = load16(Qs + off);
-          if (DO_DK) da[kc] = load16(Ds + off);
+          qa[kc] = *reinterpret_cast<const u32x4*>(Qb + rd_ofs[rb * NKC + kc]);
+          if (DO_DK) da[kc] = *reinterpret_cast<const u32x4*>(Db + rd_ofs[rb * NKC + kc]);
         }
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
@@ -618,8 +649,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
       for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          if (DO_DV) ta_v[cc * NDB + db] = tr_operand<D>(Ds, lane, cc, db * 32);
-          if (DO_DK) ta_k[cc * NDB + db] = tr_operand<D>(Qs, lane, cc, db * 32);
+          if (DO_DV) ta_v[cc * NDB + db] = tr_read(Db, cc, db);
+          if (DO_DK) ta_k[cc * NDB + db] = tr_read(Qb, cc, db);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -701,19 +732,30 @@ void bwd_dkdv_kernel(const BwdParams p) {
   // barrier publishes every wave's share of it.  The barrier also retires
   // the reads of tile it - 1, whose stage the next DMA refills.
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue(s);
-  for (int it = 0; it < J; ++it) {
+  for (int s = 0; s < NS - 1; ++s) issue(s, s);
+  // Straight-line body: a tile that holds no visible (row, key) pair for
+  // this wave is computed anyway with the mask (its P is all zero).  A
+  // branch around it would make the dK / dV accumulators a join value that
+  // the compiler copies between register files on every iteration.  The
+  // loop is unrolled by the stage count, so every stage base is a constant
+  // that the LDS reads take as their immediate offset.
+  auto iteration = [&](int it, int stage) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPS));
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue(it + NS - 1);
-    // Straight-line body: a tile that holds no visible (row, key) pair for
-    // this wave is computed anyway with the mask (its P is all zero).  A
-    // branch around it would make the dK / dV accumulators a join value that
-    // the compiler copies between register files on every iteration.
-    tile_math(it, it % NS, wave_masks(m0_of(it)));
+    issue(it + NS - 1, (stage + NS - 1) % NS);
+    tile_math(it, stage, wave_masks(m0_of(it)));
+  };
+  static_assert(NS == 3, "the main loop is unrolled for three stages");
+  int it = 0;
+  for (; it + NS <= J; it += NS) {
+    iteration(it, 0);
+    iteration(it + 1, 1);
+    iteration(it + 2, 2);
   }
+  if (it < J) iteration(it, 0);
+  if (it + 1 < J) iteration(it + 1, 1);
   // No DMA may still be writing LDS when the workgroup retires.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 

@@ -195,10 +195,12 @@ __device__ inline uint32_t lds_address(const void* p) {
 // inline assembly so that the compiler does not treat every later LDS read as
 // dependent on it and wait for all outstanding loads; the kernel waits for
 // these loads itself (s_waitcnt vmcnt) before the barrier that publishes them.
+// (The readfirstlane states the uniformity the "s" constraint needs: the
+// compiler does not always prove it for a computed address.)
 __device__ inline void buf_load16_lds(const u32x4& r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
-               : "s"(lds), "v"(voff), "s"(r)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 
@@ -206,7 +208,7 @@ __device__ inline void buf_load16_lds(const u32x4& r, uint32_t lds, uint32_t vof
 __device__ inline void buf_load4_lds(const u32x4& r, uint32_t lds, uint32_t voff) {
   asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
                :
-               : "s"(lds), "v"(voff), "s"(r)
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r)
                : "memory", "m0");
 }
 
