@@ -276,29 +276,7 @@ void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
 
-  // Per-lane byte offsets within a stage, computed once (K and V tiles share
-  // them): row reads of S^T / dP^T (row kb*32 + c32, chunk 2 kc + g) and the
-  // two halves of each transposed K read of dQ^T.
   constexpr bool STAGE = D <= 128;
-  uint32_t rd_ofs[STAGE ? NKB * NKC : 1];
-  uint32_t tr_ofs[STAGE ? NCC * NDB * 2 : 1];
-  if constexpr (STAGE) {
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-      for (int kc = 0; kc < NKC; ++kc)
-        rd_ofs[kb * NKC + kc] = 2u * (uint32_t)swz_off<D>(kb * 32 + c32, 2 * kc + g);
-    const int j = lane & 15;
-#pragma unroll
-    for (int cc = 0; cc < NCC; ++cc)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int r = 16 * cc + 4 * g + (j >> 2);
-        const int d = db * 32 + 16 * (c32 >> 4) + 4 * (j & 3);
-        tr_ofs[(cc * NDB + db) * 2] = 2u * (uint32_t)(swz_off<D>(r, d >> 3) + (d & 7));
-        tr_ofs[(cc * NDB + db) * 2 + 1] = 2u * (uint32_t)(swz_off<D>(r + 8, d >> 3) + (d & 7));
-      }
-  }
 
   // One tile: operands staged ahead of their products (all A operands of a
   // 32-key block of S^T / dP^T first; the transposed K reads of dQ^T before
@@ -306,8 +284,6 @@ void bwd_dq_kernel(const BwdParams p) {
   auto tile_math = [&](int t, int stage, bool masked) {
     const uint16_t* Ks = reinterpret_cast<const uint16_t*>(smem_b + stage * TILEB);
     const uint16_t* Vs = reinterpret_cast<const uint16_t*>(smem_b + (NS + stage) * TILEB);
-    const uint8_t* Kb = reinterpret_cast<const uint8_t*>(Ks);
-    const uint8_t* Vb = reinterpret_cast<const uint8_t*>(Vs);
     f32x16 s[NKB], dp[NKB];
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
@@ -317,8 +293,9 @@ void bwd_dq_kernel(const BwdParams p) {
         u32x4 ka[NKC], va[NKC];
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
-          ka[kc] = *reinterpret_cast<const u32x4*>(Kb + rd_ofs[kb * NKC + kc]);
-          va[kc] = *reinterpret_cast<const u32x4*>(Vb + rd_ofs[kb * NKC + kc]);
+          const int off = swz_off<D>(kb * 32 + c32, 2 * kc + g);
+          ka[kc] = load16(Ks + off);
+          va[kc] = load16(Vs + off);
         }
 #pragma unroll
         for (int kc = 0; kc < NKC; ++kc) {
@@ -349,12 +326,7 @@ void bwd_dq_kernel(const BwdParams p) {
 #pragma unroll
       for (int cc = 0; cc < NCC; ++cc)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_ofs[(cc * NDB + db) * 2]));
-          const u32x2 hi =
-              lds_read_tr16(reinterpret_cast<const uint16_t*>(Kb + tr_ofs[(cc * NDB + db) * 2 + 1]));
-          ta[cc * NDB + db] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        }
+        for (int db = 0; db < NDB; ++db) ta[cc * NDB + db] = tr_operand<D>(Ks, lane, cc, db * 32);
       __builtin_amdgcn_sched_barrier(0);
     }
     const int n0 = t * BN;
@@ -404,8 +376,9 @@ void bwd_dq_kernel(const BwdParams p) {
   // Tiles it .. it + NS - 2 are in flight at the top of iteration it; the
   // barrier after the wait publishes tile it and retires the reads of tile
   // it - 1, whose stage the next DMA refills.  The body is straight-line (a
-  // wave whose rows see no key of a tile computes it masked) and unrolled by
-  // the stage count, so the stage bases are immediate offsets of the reads.
+  // wave whose rows see no key of a tile computes it masked).  With staged
+  // operands it is unrolled by the stage count, so the stage bases are
+  // immediate offsets of the reads.
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s) issue(s, s);
   auto iteration = [&](int it, int stage) {
@@ -416,15 +389,19 @@ void bwd_dq_kernel(const BwdParams p) {
     issue(it + NS - 1, (stage + NS - 1) % NS);
     tile_math(t_begin + it, stage, wave_masks(t_begin + it));
   };
-  static_assert(NS == 3, "the main loop is unrolled for three stages");
-  int it = 0;
-  for (; it + NS <= J; it += NS) {
-    iteration(it, 0);
-    iteration(it + 1, 1);
-    iteration(it + 2, 2);
+  if constexpr (STAGE) {
+    static_assert(NS == 3, "the main loop is unrolled for three stages");
+    int it = 0;
+    for (; it + NS <= J; it += NS) {
+      iteration(it, 0);
+      iteration(it + 1, 1);
+      iteration(it + 2, 2);
+    }
+    if (it < J) iteration(it, 0);
+    if (it + 1 < J) iteration(it + 1, 1);
+  } else {
+    for (int it = 0; it < J; ++it) iteration(it, it % NS);
   }
-  if (it < J) iteration(it, 0);
-  if (it + 1 < J) iteration(it + 1, 1);
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // ------------------------------------------------------------ dQ = scale * acc
@@ -786,15 +763,19 @@ void bwd_dkdv_kernel(const BwdParams p) {
     issue(it + NS - 1, (stage + NS - 1) % NS);
     tile_math(it, stage, wave_masks(m0_of(it)));
   };
-  static_assert(NS == 3, "the main loop is unrolled for three stages");
-  int it = 0;
-  for (; it + NS <= J; it += NS) {
-    iteration(it, 0);
-    iteration(it + 1, 1);
-    iteration(it + 2, 2);
+  if constexpr (STAGE) {
+    static_assert(NS == 3, "the main loop is unrolled for three stages");
+    int it = 0;
+    for (; it + NS <= J; it += NS) {
+      iteration(it, 0);
+      iteration(it + 1, 1);
+      iteration(it + 2, 2);
+    }
+    if (it < J) iteration(it, 0);
+    if (it + 1 < J) iteration(it + 1, 1);
+  } else {
+    for (int it = 0; it < J; ++it) iteration(it, it % NS);
   }
-  if (it < J) iteration(it, 0);
-  if (it + 1 < J) iteration(it + 1, 1);
   // No DMA may still be writing LDS when the workgroup retires.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
