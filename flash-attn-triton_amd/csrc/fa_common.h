@@ -126,6 +126,28 @@ __device__ inline void work_item(int L, int total, int n_mblocks, bool heavy_fir
   if (heavy_first) mb = n_mblocks - 1 - mb;
 }
 
+// Work item of a varlen launch, whose groups differ in work (their
+// sequences' lengths): contiguous group ranges per XCD would load the XCDs
+// unevenly (1.56x the mean on the busiest XCD at 32 random lengths).  Here
+// XCD x owns the K/V heads c = grp / group with c % 8 == x, so the sequences
+// spread over all XCDs while the query heads of one K/V head share its tiles
+// in one L2, and runs them one K/V head at a time (row blocks of the head's
+// query heads interleaved, the last first when heavy_first).  Returns false
+// (no item assigned) unless the K/V heads split evenly over the XCDs.
+__device__ inline bool work_item_kv_rr(int L, int total, int n_mblocks, int group,
+                                       bool heavy_first, int& mb, int& grp) {
+  constexpr int kXcds = 8;
+  const int per_kv = group * n_mblocks;   // items per K/V head
+  if (per_kv <= 0 || total % (kXcds * per_kv) != 0) return false;
+  const int k = L / kXcds;
+  const int c = (k / per_kv) * kXcds + L % kXcds;
+  const int r = k % per_kv;
+  mb = r / group;
+  if (heavy_first) mb = n_mblocks - 1 - mb;
+  grp = c * group + r % group;
+  return true;
+}
+
 // work_item span of the causal launches of the ping-pong forward, INT8 and
 // backward kernels: 4 groups measured best on MI355X at B=4 H=32 S=4096 (1:
 // 5-7% slower, all groups of an XCD: 1-3% slower).

@@ -87,11 +87,15 @@ void prefill_kernel(const FwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
-  // Span 1 (a group's row blocks back to back, heaviest first): ragged varlen
-  // sequences keep their K/V in L2 one group at a time; the wider span of the
-  // ping-pong kernels doubled the HBM reads at the varlen configuration.
+  // Varlen: K/V heads dealt round-robin over the XCDs (ragged sequences would
+  // load contiguous ranges unevenly), each K/V head's row blocks back to
+  // back.  Otherwise span 1 (a group's row blocks back to back, heaviest
+  // first): the wider span of the ping-pong kernels doubled the HBM reads at
+  // the varlen configuration.
   int mb, id;
-  work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.heavy_first != 0, 1, mb, id);
+  if (p.cu_q == nullptr ||
+      !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_mblocks, p.group, p.heavy_first != 0, mb, id))
+    work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.heavy_first != 0, 1, mb, id);
   const int hh = id % p.heads_q;
   const int b = id / p.heads_q;
   const int kvh = hh / p.group;
