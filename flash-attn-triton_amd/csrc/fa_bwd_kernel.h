@@ -156,9 +156,13 @@ void bwd_dq_kernel(const BwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
-  // Causal: late (longer) rows first.
+  // Causal: late (longer) rows first.  Varlen: K/V heads round-robin over
+  // the XCDs, as in the forward (ragged sequences load contiguous ranges
+  // unevenly).
   int mb, id;
-  work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, mb, id);
+  if (p.cu_q == nullptr ||
+      !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_blocks, p.group, p.causal != 0, mb, id))
+    work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, mb, id);
   const int hh = id % p.heads_q;
   const int b = id / p.heads_q;
   const int kvh = hh / p.group;
@@ -461,9 +465,12 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
-  // Causal: early key blocks (seen by the most rows) first.
+  // Causal: early key blocks (seen by the most rows) first.  Varlen: K/V
+  // heads round-robin over the XCDs.
   int nb, id;
-  work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, nb, id);
+  if (p.cu_q == nullptr ||
+      !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_blocks, 1, p.causal != 0, nb, id))
+    work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, nb, id);
   if (p.causal) nb = p.n_blocks - 1 - nb;
   const int kvh = id % p.heads_k;
   const int b = id / p.heads_k;

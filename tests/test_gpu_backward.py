@@ -175,6 +175,14 @@ def test_varlen_empty_sequences_and_features():
                  window=(64, 0), softcap=30.0, alibi=True, seed=91)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_kv_heads_over_xcds(causal):
+    # 4 sequences x 2 K/V heads = 8 K/V heads: the launches deal them
+    # round-robin over the 8 XCDs (GQA group 2 for dQ); ragged lengths.
+    _varlen_case([300, 7, 129, 64], [300, 40, 129, 200], Hq=4, Hk=2, D=128, causal=causal,
+                 seed=97)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_varlen_dtypes_d128(dtype):
     _varlen_case([200, 513], [200, 513], Hq=4, Hk=4, D=128, dtype=dtype, causal=True, seed=95)

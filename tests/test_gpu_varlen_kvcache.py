@@ -53,6 +53,14 @@ def test_varlen_empty_sequences():
     _varlen_case([0, 20, 33, 7], [5, 0, 40, 7], causal=True, seed=21)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_varlen_kv_heads_over_xcds(causal):
+    # 4 sequences x 2 K/V heads = 8 K/V heads, dealt round-robin over the 8
+    # XCDs; GQA group 4, ragged lengths, one empty query sequence.
+    _varlen_case([300, 0, 129, 640], [300, 40, 129, 200], hq=8, hk=2, d=128, causal=causal,
+                 seed=35)
+
+
 def test_varlen_gqa_window_alibi_softcap():
     H = 8
     slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).expand(3, H).contiguous().float()
