@@ -95,8 +95,12 @@ void prefill_pp_kernel(const FwdParams p) {
   const int g = lane >> 5;
 
   // ------------------------------------------------------------ work item
+  // Varlen: K/V heads round-robin over the XCDs (ragged sequences load
+  // contiguous group ranges unevenly).
   int mb, id;
-  work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.heavy_first != 0, kCausalSpan, mb, id);
+  if (p.cu_q == nullptr ||
+      !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_mblocks, p.group, p.heavy_first != 0, mb, id))
+    work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.heavy_first != 0, kCausalSpan, mb, id);
   const int hh = id % p.heads_q;
   const int b = id / p.heads_q;
   const int kvh = hh / p.group;
