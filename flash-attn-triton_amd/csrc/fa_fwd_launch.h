@@ -67,10 +67,10 @@ hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
 }
 
 // Ping-pong prefill (fa_prefill_pp.h): 8 waves, 256 query rows per workgroup.
-template <class T, int D>
+template <class T, int D, bool VARLEN>
 hipError_t launch_prefill_pp(FwdParams p, hipStream_t st) {
   using Tile = PingPongTile<D>;
-  auto kern = prefill_pp_kernel<T, D>;
+  auto kern = prefill_pp_kernel<T, D, VARLEN>;
   static bool lds_attr_set = false;
   if (!lds_attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
@@ -104,7 +104,10 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
     // kernel is 1.22x slower there (its 256-row blocks visit every key tile
     // of the block's window for all rows, and the softmax phase outgrows the
     // GEMM phase).
-    if constexpr (!GEN) return launch_prefill_pp<T, D>(p, st);
+    if constexpr (!GEN) {
+      return p.cu_q != nullptr ? launch_prefill_pp<T, D, true>(p, st)
+                               : launch_prefill_pp<T, D, false>(p, st);
+    }
     // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
     // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves.
     if (masked) {

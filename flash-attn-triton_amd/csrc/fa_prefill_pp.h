@@ -67,7 +67,9 @@ __device__ inline void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <class T, int D>
+// VARLEN: cu_seqlens addressing (an instantiation of its own, so that the
+// dense kernel carries none of its work-item code).
+template <class T, int D, bool VARLEN>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_pp_kernel(const FwdParams p) {
   using Tile = PingPongTile<D>;
@@ -98,7 +100,7 @@ void prefill_pp_kernel(const FwdParams p) {
   // Varlen: K/V heads round-robin over the XCDs (ragged sequences load
   // contiguous group ranges unevenly).
   int mb, id;
-  if (p.cu_q == nullptr ||
+  if (!VARLEN ||
       !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_mblocks, p.group, p.heavy_first != 0, mb, id))
     work_item(blockIdx.x, p.total_blocks, p.n_mblocks, p.heavy_first != 0, kCausalSpan, mb, id);
   const int hh = id % p.heads_q;
