@@ -132,16 +132,24 @@ __device__ inline void work_item(int L, int total, int n_mblocks, bool heavy_fir
 // XCD x owns the K/V heads c = grp / group with c % 8 == x, so the sequences
 // spread over all XCDs while the query heads of one K/V head share its tiles
 // in one L2, and runs them one K/V head at a time (row blocks of the head's
-// query heads interleaved, the last first when heavy_first).  Returns false
-// (no item assigned) unless the K/V heads split evenly over the XCDs.
+// query heads interleaved, the last first when heavy_first).  The last
+// n_kv % 8 K/V heads, if any, follow with their items spread over all XCDs.
+// Returns false (no item assigned) unless total = n_kv * group * n_mblocks.
 __device__ inline bool work_item_kv_rr(int L, int total, int n_mblocks, int group,
                                        bool heavy_first, int& mb, int& grp) {
   constexpr int kXcds = 8;
   const int per_kv = group * n_mblocks;   // items per K/V head
-  if (per_kv <= 0 || total % (kXcds * per_kv) != 0) return false;
-  const int k = L / kXcds;
-  const int c = (k / per_kv) * kXcds + L % kXcds;
-  const int r = k % per_kv;
+  if (per_kv <= 0 || total % per_kv != 0) return false;
+  const int main_items = total / per_kv / kXcds * kXcds * per_kv;
+  int c, r;
+  if (L < main_items) {
+    const int k = L / kXcds;
+    c = (k / per_kv) * kXcds + L % kXcds;
+    r = k % per_kv;
+  } else {
+    c = L / per_kv;   // main_items is a multiple of per_kv
+    r = L % per_kv;
+  }
   mb = r / group;
   if (heavy_first) mb = n_mblocks - 1 - mb;
   grp = c * group + r % group;
