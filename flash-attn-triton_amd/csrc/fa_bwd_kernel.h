@@ -139,7 +139,9 @@ struct BwdDqTile {
   static_assert(IPW * NW == 2 * IPS && IPW > 0, "K and V tiles must split evenly over the waves");
 };
 
-template <class T, int D, int NW, int BN, int NS, bool GENERIC, int WPE>
+// VARLEN: cu_seqlens launch (an instantiation of its own, so that the dense
+// kernel carries none of the varlen work-item code).
+template <class T, int D, int NW, int BN, int NS, bool GENERIC, int WPE, bool VARLEN>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void bwd_dq_kernel(const BwdParams p) {
   using Tile = BwdDqTile<T, D, NW, BN, NS>;
@@ -160,7 +162,7 @@ void bwd_dq_kernel(const BwdParams p) {
   // the XCDs, as in the forward (ragged sequences load contiguous ranges
   // unevenly).
   int mb, id;
-  if (p.cu_q == nullptr ||
+  if (!VARLEN ||
       !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_blocks, p.group, p.causal != 0, mb, id))
     work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, mb, id);
   const int hh = id % p.heads_q;
@@ -445,7 +447,7 @@ struct BwdDkvTile {
 // PASS 0 accumulates dK and dV together; at D = 256 the two accumulators do
 // not fit beside K and V, so the launcher runs PASS 1 (dV only) and PASS 2 (dK
 // only), recomputing S in each.
-template <class T, int D, int NW, int BM, int NS, bool GENERIC, int WPE, int PASS>
+template <class T, int D, int NW, int BM, int NS, bool GENERIC, int WPE, int PASS, bool VARLEN>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void bwd_dkdv_kernel(const BwdParams p) {
   constexpr bool DO_DV = PASS != 2, DO_DK = PASS != 1;
@@ -468,7 +470,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
   // Causal: early key blocks (seen by the most rows) first.  Varlen: K/V
   // heads round-robin over the XCDs.
   int nb, id;
-  if (p.cu_q == nullptr ||
+  if (!VARLEN ||
       !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_blocks, 1, p.causal != 0, nb, id))
     work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, nb, id);
   if (p.causal) nb = p.n_blocks - 1 - nb;

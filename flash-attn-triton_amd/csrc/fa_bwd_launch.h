@@ -26,11 +26,11 @@ hipError_t set_lds(Kern kern, int bytes, bool& done) {
   return e;
 }
 
-template <class T, int D, bool GEN, int PASS>
+template <class T, int D, bool GEN, int PASS, bool VARLEN>
 hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
   using Tile = BwdDkvTile<T, D, C::KV_NW, C::KV_BM, C::KV_NS>;
-  auto kern = bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, C::KV_NS, GEN, C::KV_WPE, PASS>;
+  auto kern = bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, C::KV_NS, GEN, C::KV_WPE, PASS, VARLEN>;
   // The ALiBi slope table (one float per query head of the group) follows the
   // stages; the attribute allows the largest table that still fits.
   constexpr int kMaxLds = 160 * 1024;
@@ -48,12 +48,12 @@ hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <class T, int D, bool GEN>
-hipError_t launch_bwd_d(BwdParams p, hipStream_t st) {
+template <class T, int D, bool GEN, bool VARLEN>
+hipError_t launch_bwd_v(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
   {
     using Tile = BwdDqTile<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS>;
-    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS, GEN, C::DQ_WPE>;
+    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS, GEN, C::DQ_WPE, VARLEN>;
     static bool lds_set = false;
     hipError_t e = set_lds(kern, Tile::LDS_BYTES, lds_set);
     if (e != hipSuccess) return e;
@@ -68,12 +68,18 @@ hipError_t launch_bwd_d(BwdParams p, hipStream_t st) {
     }
   }
   if constexpr (D >= 256) {
-    hipError_t e = launch_dkdv<T, D, GEN, 1>(p, st);
+    hipError_t e = launch_dkdv<T, D, GEN, 1, VARLEN>(p, st);
     if (e != hipSuccess) return e;
-    return launch_dkdv<T, D, GEN, 2>(p, st);
+    return launch_dkdv<T, D, GEN, 2, VARLEN>(p, st);
   } else {
-    return launch_dkdv<T, D, GEN, 0>(p, st);
+    return launch_dkdv<T, D, GEN, 0, VARLEN>(p, st);
   }
+}
+
+template <class T, int D, bool GEN>
+hipError_t launch_bwd_d(const BwdParams& p, hipStream_t st) {
+  return p.cu_q != nullptr ? launch_bwd_v<T, D, GEN, true>(p, st)
+                           : launch_bwd_v<T, D, GEN, false>(p, st);
 }
 
 template <class T>
