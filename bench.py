@@ -24,8 +24,19 @@ combine kernels together), against the MI355X published peak.
 ``roofline.traffic`` is HBM bytes per launch from two ``rocprofv3 --pmc`` child
 runs (FETCH_SIZE, WRITE_SIZE), each scaled by what the same counter reads for
 a 1 GiB device copy; ``--traffic off`` skips them.  ``cpu_baseline`` is the
-float64 numpy oracle timed on a bounded sample of the same workload with at
-most 16 host threads.
+CPU SDPA path the metric names: ``torch.nn.functional.scaled_dot_product_attention``
+in fp32 on the host's cores (at most 16 threads), timed on a bounded sample
+of the same workload (decode: block-table gather + SDPA with ``enable_gqa``
+per sequence, gather included; varlen: the same score pipeline per sequence
+in fp32 torch math, since softcap is not an SDPA mask; backward: autograd of
+SDPA).
+
+The default run (the headline, dense FP16 causal) also measures the other
+targets of the metric in the same line, under ``extra`` (``--extras off``
+skips them): dense FP16 non-causal, INT8-QK causal and non-causal (BASELINE
+config 3, with their speed ratio to FP16 at the same shape and mask, per
+launch and whole job) and paged decode GB/s (config 4).  Each extra carries
+its whole-job value, mean launch time, roofline fraction and CPU baseline.
 """
 from __future__ import annotations
 
@@ -51,6 +62,62 @@ def _randn(torch, shape, seed, dtype, device):
     return torch.randn(*shape, generator=gen, device=device, dtype=torch.float32).to(dtype)
 
 
+# ----------------------------------------------------------------------------- CPU baseline
+def _median_time(fn, reps=3):
+    """1 untimed run, then the median of ``reps`` timed runs (seconds)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _cpu_heads(torch, tensors, n_heads, head_axis):
+    """fp32 CPU copies [1, n, S, D] of the first ``n_heads`` (batch, head) pairs
+    of BSHD (head_axis 2) or BHSD (head_axis 1) tensors."""
+    out = []
+    for t in tensors:
+        x = t.transpose(1, 2) if head_axis == 2 else t   # -> [B, H, S, D]
+        B, H = x.shape[0], x.shape[1]
+        x = x.reshape(B * H, x.shape[2], x.shape[3])[:n_heads]
+        out.append(x.float().cpu().unsqueeze(0).contiguous())
+    return out
+
+
+def cpu_sdpa_dense(torch, tensors, head_axis, causal, flops_per_head, n_total, budget_s,
+                   what, backward=False, dout=None):
+    """fp32 SDPA (or its autograd backward) on the host over a sample of
+    (batch, head) pairs sized to about ``budget_s`` seconds of work."""
+    import torch.nn.functional as F
+    torch.set_num_threads(CPU_THREADS)
+
+    def run(n):
+        q, k, v = _cpu_heads(torch, tensors, n, head_axis)
+        if not backward:
+            return lambda: F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+        (g,) = _cpu_heads(torch, [dout], n, head_axis)
+        q.requires_grad_(True); k.requires_grad_(True); v.requires_grad_(True)
+
+        def bwd():
+            out = F.scaled_dot_product_attention(q, k, v, is_causal=causal)
+            out.backward(g)
+            q.grad = k.grad = v.grad = None
+        return bwd
+
+    t1 = _median_time(run(1), reps=1)
+    n = int(max(1, min(n_total, budget_s / 4.0 / max(t1, 1e-6))))
+    dt = _median_time(run(n))
+    flops = flops_per_head * n
+    return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": CPU_THREADS,
+            "kind": "port",
+            "sample": f"torch.nn.functional.scaled_dot_product_attention fp32 on CPU "
+                      f"({'autograd backward of ' if backward else ''}{what}), {n} of {n_total} "
+                      f"(batch, head) pairs as one [1, {n}, S, D] call, median of 3 after 1 "
+                      f"warmup: {dt * 1e3:.1f} ms; torch.set_num_threads({CPU_THREADS})"}
+
+
 # ----------------------------------------------------------------------------- workloads
 def make_dense(torch, causal):
     from flash_attn_triton import flash_attn_func
@@ -62,21 +129,8 @@ def make_dense(torch, causal):
         return flash_attn_func(q, k, v, causal=causal)
 
     def cpu(budget_s):
-        import numpy as np
-        from oracle import attention as ora
-        heads, t0 = 0, time.perf_counter()
-        while heads < B * H and (time.perf_counter() - t0) < budget_s:
-            b, h = divmod(heads, H)
-            qc, kc, vc = (t[b:b + 1, :, h:h + 1].cpu().numpy() for t in (q, k, v))
-            ora.attention(qc, kc, vc, causal=causal)
-            heads += 1
-        dt = time.perf_counter() - t0
-        per_head = flops / (B * H)
-        return {"value": per_head * heads / dt / 1e12, "unit": "TFLOP/s",
-                "cores": CPU_THREADS, "kind": "port",
-                "sample": f"float64 numpy oracle (oracle/attention.py) on {heads} of {B * H} "
-                          f"(batch, head) pairs, S=4096, D=128, causal={causal}; "
-                          f"{dt:.1f} s; {CPU_THREADS} BLAS threads"}
+        return cpu_sdpa_dense(torch, (q, k, v), 2, causal, flops / (B * H), B * H, budget_s,
+                              f"S=4096, D=128, causal={causal}")
 
     cfg = {"workload": f"dense_fp16_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
            "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
@@ -103,19 +157,12 @@ def make_bwd(torch, causal):
         return dense_backward(q, k, v, out, do, lse, softmax_scale=scale, causal=causal)
 
     def cpu(budget_s):
-        from oracle import attention as ora
-        heads, t0 = 0, time.perf_counter()
-        while heads < B * H and (time.perf_counter() - t0) < budget_s:
-            b, h = divmod(heads, H)
-            qc, kc, vc, dc = (t[b:b + 1, :, h:h + 1].cpu().numpy() for t in (q, k, v, do))
-            ora.attention_backward(qc, kc, vc, dc, scale, causal)
-            heads += 1
-        dt = time.perf_counter() - t0
-        return {"value": flops / (B * H) * heads / dt / 1e12, "unit": "TFLOP/s",
-                "cores": CPU_THREADS, "kind": "port",
-                "sample": f"float64 numpy oracle gradients (oracle/attention.py "
-                          f"attention_backward) on {heads} of {B * H} (batch, head) pairs, "
-                          f"S=4096, D=128, causal={causal}; {dt:.1f} s; {CPU_THREADS} BLAS threads"}
+        # The timed CPU call is forward + backward (autograd has no backward
+        # alone); its rate counts the backward's 2.5x FLOPs, so it flatters the
+        # CPU by the forward's share.
+        return cpu_sdpa_dense(torch, (q, k, v), 2, causal, flops / (B * H), B * H, budget_s,
+                              f"S=4096, D=128, causal={causal}; forward included in the time",
+                              backward=True, dout=do)
 
     cfg = {"workload": f"dense_bwd_fp16_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
            "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
@@ -142,18 +189,9 @@ def make_int8(torch, causal):
         return attention_int8(q, k, v, causal=causal)
 
     def cpu(budget_s):
-        from oracle import quant
-        heads, t0 = 0, time.perf_counter()
-        while heads < B * H and (time.perf_counter() - t0) < budget_s:
-            b, h = divmod(heads, H)
-            qc, kc, vc = (t[b:b + 1, h:h + 1].cpu().numpy() for t in (q, k, v))
-            quant.attention_int8(qc, kc, vc.astype("float64"), causal=causal)
-            heads += 1
-        dt = time.perf_counter() - t0
-        return {"value": flops / (B * H) * heads / dt / 1e12, "unit": "TFLOP/s",
-                "cores": CPU_THREADS, "kind": "port",
-                "sample": f"numpy INT8-QK oracle (oracle/quant.py) on {heads} of {B * H} "
-                          f"(batch, head) pairs, S=4096, D=128; {dt:.1f} s"}
+        # The host has no INT8 attention: fp32 SDPA of the same shape and mask.
+        return cpu_sdpa_dense(torch, (q, k, v), 1, causal, flops / (B * H), B * H, budget_s,
+                              f"S=4096, D=128, causal={causal}, same inputs as the INT8 run")
 
     cfg = {"workload": f"int8qk_{'causal' if causal else 'noncausal'}_b{B}_h{H}_s{S}_d{D}",
            "batch": B, "heads": H, "seqlen": S, "head_dim": D, "causal": causal,
@@ -190,19 +228,36 @@ def make_decode(torch):
         return flash_attn_with_kvcache(q, kc, vc, cache_seqlens=seqlens, block_table=btd)
 
     def cpu(budget_s):
-        from oracle import attention as ora
-        qn, kn, vn = q.cpu().numpy(), kc.cpu().numpy(), vc.cpu().numpy()
-        done_bytes, b, t0 = 0, 0, time.perf_counter()
+        # Per sequence: gather its pages through the block table, then SDPA with
+        # enable_gqa (the gather is inside the timing).  The host caches are
+        # fp32, so the CPU reads twice the fp16 bytes the rate is quoted in.
+        import torch.nn.functional as F
+        torch.set_num_threads(CPU_THREADS)
+        kh, vh, qh = kc.float().cpu(), vc.float().cpu(), q.float().cpu()
+        btl = bt.long()
+
+        def one(b):
+            L = int(lengths[b])
+            pg = btl[b, :pages_per[b]]
+            k = kh[pg].reshape(-1, Hk, D)[:L].transpose(0, 1).unsqueeze(0)
+            v = vh[pg].reshape(-1, Hk, D)[:L].transpose(0, 1).unsqueeze(0)
+            return F.scaled_dot_product_attention(qh[b:b + 1].transpose(1, 2), k, v,
+                                                  enable_gqa=True)
+
+        one(0)
+        done, b, t0 = 0, 0, time.perf_counter()
         while b < B and (time.perf_counter() - t0) < budget_s:
-            ora.attention_kvcache(qn[b:b + 1], kn, vn, cache_seqlens=[int(lengths[b])],
-                                  block_table=bt[b:b + 1].numpy())
-            done_bytes += int(lengths[b]) * Hk * D * 2 * 2
+            one(b)
+            done += int(lengths[b]) * Hk * D * 2 * 2 + Hq * D * 2 * 2 + pages_per[b] * 4 + 4
             b += 1
         dt = time.perf_counter() - t0
-        return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": CPU_THREADS,
+        return {"value": round(done / dt / 1e9, 4), "unit": "GB/s", "cores": CPU_THREADS,
                 "kind": "port",
-                "sample": f"float64 numpy oracle (gather through the block table + attention) on "
-                          f"{b} of {B} sequences; {dt:.1f} s"}
+                "sample": f"per sequence: block-table gather + "
+                          f"torch.nn.functional.scaled_dot_product_attention(enable_gqa=True), "
+                          f"fp32 on CPU, {b} of {B} sequences in {dt:.2f} s (gather included); "
+                          f"rate in the fp16 algorithmic bytes; "
+                          f"torch.set_num_threads({CPU_THREADS})"}
 
     cfg = {"workload": "paged_decode_b64_hq32_hk8_d128_page256", "batch": B, "heads_q": Hq,
            "heads_k": Hk, "head_dim": D, "page_size": page, "total_cache_tokens": total_tokens,
@@ -225,8 +280,9 @@ def make_varlen(torch):
     slopes = (2.0 ** (-8.0 * (torch.arange(H) + 1) / H)).float().cuda()
     cud = cu.cuda()
     max_len = int(lengths.max())
+    left, cap = 1024, 30.0
 
-    def pairs(L, left=1024):
+    def pairs(L):
         i = torch.arange(L, dtype=torch.float64)
         return float(torch.clamp(i, max=left).sum() + L)
 
@@ -235,23 +291,42 @@ def make_varlen(torch):
 
     def step():
         return flash_attn_varlen_func(q, k, v, cud, cud, max_len, max_len, causal=True,
-                                      window_size=(1024, 0), softcap=30.0, alibi_slopes=slopes)
+                                      window_size=(left, 0), softcap=cap, alibi_slopes=slopes)
 
     def cpu(budget_s):
-        from oracle import attention as ora
-        qn, kn, vn = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
-        sl = slopes.cpu().numpy()
+        # softcap is not an additive mask, so the host runs SDPA's math as
+        # fp32 torch ops per sequence: scores, ALiBi, softcap, causal + window
+        # mask, softmax, product with V.
+        torch.set_num_threads(CPU_THREADS)
+        qh, kh, vh = (t.float().cpu() for t in (q, k, v))
+        sl = slopes.cpu()
+        scale = 1.0 / math.sqrt(D)
+
+        def one(b):
+            s, e = int(cu[b]), int(cu[b + 1])
+            L = e - s
+            qs, ks, vs = (t[s:e].transpose(0, 1) for t in (qh, kh, vh))   # [H, L, D]
+            sc = torch.matmul(qs, ks.transpose(1, 2)) * scale
+            i = torch.arange(L)
+            dist = (i[:, None] - i[None, :]).float()
+            sc = sc - sl[:, None, None] * dist.abs()
+            sc = cap * torch.tanh(sc / cap)
+            keep = (dist >= 0) & (dist <= left)
+            sc = sc.masked_fill(~keep, float("-inf"))
+            return torch.matmul(torch.softmax(sc, dim=-1), vs)
+
+        one(0)
         done, b, t0 = 0.0, 0, time.perf_counter()
         while b < 32 and (time.perf_counter() - t0) < budget_s:
-            s, e = int(cu[b]), int(cu[b + 1])
-            ora.attention(qn[None, s:e], kn[None, s:e], vn[None, s:e], None, True, (1024, 0),
-                          30.0, sl)
-            done += 4.0 * H * D * pairs(e - s)
+            one(b)
+            done += 4.0 * H * D * pairs(int(cu[b + 1] - cu[b]))
             b += 1
         dt = time.perf_counter() - t0
-        return {"value": done / dt / 1e12, "unit": "TFLOP/s", "cores": CPU_THREADS,
+        return {"value": round(done / dt / 1e12, 5), "unit": "TFLOP/s", "cores": CPU_THREADS,
                 "kind": "port",
-                "sample": f"float64 numpy oracle on {b} of 32 sequences; {dt:.1f} s"}
+                "sample": f"SDPA math in fp32 torch ops on CPU per sequence (scores, ALiBi, "
+                          f"softcap, causal + window mask, softmax, PV), {b} of 32 sequences "
+                          f"in {dt:.2f} s; torch.set_num_threads({CPU_THREADS})"}
 
     cfg = {"workload": "varlen_fp16_32seq_h16_d128_causal_win1024_alibi_softcap30",
            "sequences": 32, "total_tokens": T, "heads": H, "head_dim": D,
@@ -338,7 +413,7 @@ def _pmc_pass(workload, counter, kernels, outdir):
     d = os.path.join(outdir, f"{workload}_{counter}")
     cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
            sys.executable, os.path.abspath(__file__), "--workload", workload, "--steps", "2",
-           "--warmup", "1", "--cpu-budget", "0", "--traffic", "off"]
+           "--warmup", "1", "--cpu-budget", "0", "--traffic", "off", "--extras", "off"]
     subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=180,
                    check=True)
     found = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
@@ -415,19 +490,60 @@ class _LaunchTimer:
         return sum(ms) / len(ms) / 1e3 if ms else None
 
 
+def measure(torch, wl, steps, warmup):
+    """Whole-job time of ``steps`` steps after ``warmup`` untimed ones, and the
+    mean launch time of the dominant kernel inside the timed region."""
+    step = wl["step"]
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with _LaunchTimer(torch, wl["native"]) as timer:
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    avg_launch_s = timer.mean_s()
+    if avg_launch_s is None:   # copy calibration: no native entry point
+        avg_launch_s = wall / steps
+    achieved = wl["work"] / avg_launch_s / wl["scale"]
+    return {
+        "wall": wall,
+        "ms_per_step": wall / steps * 1e3,
+        "value": wl["work"] / (wall / steps) / wl["scale"],
+        "avg_launch_s": avg_launch_s,
+        "achieved": achieved,
+        "frac": achieved / wl["peak"],
+    }
+
+
+def run_cpu(torch, wl, budget):
+    if budget <= 0 or wl["cpu"] is None:
+        return None
+    from threadpoolctl import threadpool_limits
+    with threadpool_limits(limits=CPU_THREADS):
+        return wl["cpu"](budget)
+
+
+# The other targets of the metric, measured with the headline in the default run.
+EXTRAS = ("dense", "int8_causal", "int8", "decode")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="dense_causal", choices=sorted(WORKLOADS))
-    ap.add_argument("--cpu-budget", type=float, default=12.0,
-                    help="seconds of host work for the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-budget", type=float, default=8.0,
+                    help="seconds of host work for each CPU baseline sample (0 = skip)")
     ap.add_argument("--traffic", default="auto", choices=("auto", "off"),
                     help="auto: two rocprofv3 --pmc child runs (FETCH_SIZE, WRITE_SIZE) plus a "
                          "copy calibration give roofline.traffic; off: traffic null")
     ap.add_argument("--traffic-dir", default=None,
                     help="keep the counter runs' rocprofv3 output under this directory")
+    ap.add_argument("--extras", default="auto", choices=("auto", "off"),
+                    help="auto: the default workload also measures " + ", ".join(EXTRAS))
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU; every box in this pipeline has one GPU and "
@@ -448,41 +564,18 @@ def main():
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
     wl = WORKLOADS[args.workload](torch)
-    step = wl["step"]
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    torch.cuda.synchronize()
-    with _LaunchTimer(torch, wl["native"]) as timer:
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    avg_launch_s = timer.mean_s()
-    if avg_launch_s is None:   # copy calibration: no native entry point
-        avg_launch_s = wall / args.steps
-    ms_per_step = wall / args.steps * 1e3
-    value = wl["work"] / (wall / args.steps) / wl["scale"]
-    achieved = wl["work"] / avg_launch_s / wl["scale"]
-
-    cpu = None
-    if args.cpu_budget > 0 and wl["cpu"] is not None:
-        from threadpoolctl import threadpool_limits
-        torch.set_num_threads(CPU_THREADS)
-        with threadpool_limits(limits=CPU_THREADS):
-            cpu = wl["cpu"](args.cpu_budget)
+    m = measure(torch, wl, args.steps, args.warmup)
+    cpu = run_cpu(torch, wl, args.cpu_budget)
 
     roof = {
         "bound": wl["bound"],
-        "achieved": round(achieved, 3),
+        "achieved": round(m["achieved"], 3),
         "peak": round(wl["peak"], 1),
         "unit": wl["peak_unit"],
-        "frac": round(achieved / wl["peak"], 4),
+        "frac": round(m["frac"], 4),
         "traffic": None,
         "kernel": " + ".join(wl["kernels"]),
-        "avg_launch_us": round(avg_launch_s * 1e6, 2),
+        "avg_launch_us": round(m["avg_launch_s"] * 1e6, 2),
     }
     if traffic is not None:
         fetch, ffac = traffic["FETCH_SIZE"]
@@ -495,12 +588,12 @@ def main():
         roof["traffic_note"] = traffic_note
     line = {
         "metric": wl["metric"],
-        "value": round(value, 3),
+        "value": round(m["value"], 3),
         "unit": wl["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(m["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -510,6 +603,38 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
     }
+
+    if args.extras == "auto" and args.workload == "dense_causal":
+        extra = {}
+        del wl
+        runs = {"dense_causal": m}
+        for name in EXTRAS:
+            xw = WORKLOADS[name](torch)
+            xm = measure(torch, xw, args.steps, args.warmup)
+            runs[name] = xm
+            extra[name] = {
+                "metric": xw["metric"], "value": round(xm["value"], 3), "unit": xw["unit"],
+                "ms_per_step": round(xm["ms_per_step"], 4), "dtype": xw["dtype"],
+                "config": xw["config"],
+                "roofline": {"bound": xw["bound"], "achieved": round(xm["achieved"], 3),
+                             "peak": round(xw["peak"], 1), "unit": xw["peak_unit"],
+                             "frac": round(xm["frac"], 4),
+                             "kernel": " + ".join(xw["kernels"]),
+                             "avg_launch_us": round(xm["avg_launch_s"] * 1e6, 2)},
+                "cpu_baseline": run_cpu(torch, xw, args.cpu_budget),
+            }
+            if name.startswith("int8"):
+                fp16 = runs["dense_causal" if name == "int8_causal" else "dense"]
+                # Same FLOPs on both sides: the speed ratio is the time ratio.
+                extra[name]["speedup_vs_fp16"] = {
+                    "whole_job": round(fp16["ms_per_step"] / xm["ms_per_step"], 4),
+                    "per_launch": round(fp16["avg_launch_s"] / xm["avg_launch_s"], 4),
+                    "fp16_frac_of_fp16_peak": round(fp16["frac"], 4),
+                    "int8_frac_of_fp16_peak": round(xm["achieved"] / PEAK["fp16"], 4),
+                    "target": 1.3}
+            del xw
+            torch.cuda.empty_cache()
+        line["extra"] = extra
     print(json.dumps(line))
 
 

@@ -11,6 +11,7 @@
 #include <string>
 
 #include "fa_gfx950.h"
+#include "fa_api_internal.h"
 #include "fa_decode.h"
 #include "fa_probs.h"
 #include "fa_kvappend.h"
@@ -86,15 +87,19 @@ bool needs_generic(const fa::FwdParams& p) {
 }
 
 // Dropout of probability p with a 64-bit seed (the mask is defined in
-// fa_common.h); p = 0 disables it.
+// fa_common.h); p = 0 disables it.  An element is kept with probability
+// (65536 - t16) / 65536, so kept values are scaled by the reciprocal of that,
+// which makes the mask unbiased for the 16-bit threshold (1 / (1 - p) up to
+// 2^-17 / (1 - p)).  A p that rounds to t16 = 65536 would keep nothing and is
+// rejected, as is p outside [0, 1).
 bool fill_dropout(fa::DropoutCfg& d, float p, uint64_t seed) {
   if (!(p >= 0.f && p < 1.f)) return false;
-  d.enabled = p > 0.f;
+  d.t16 = (int)nearbyint((double)p * 65536.0);
+  if (d.t16 >= 65536) return false;
+  d.enabled = d.t16 > 0;
   d.seed_lo = (uint32_t)(seed & 0xffffffffu);
   d.seed_hi = (uint32_t)(seed >> 32);
-  d.t16 = (int)nearbyint((double)p * 65536.0);
-  if (d.t16 > 65536) d.t16 = 65536;
-  d.scale = (float)(1.0 / (1.0 - (double)p));
+  d.scale = (float)(65536.0 / (65536.0 - (double)d.t16));
   return true;
 }
 
@@ -170,7 +175,7 @@ int bwd_launch(const char* name, fa::BwdParams& p, int dtype, int64_t head_dim,
                int64_t alibi_batch_stride, int causal, int64_t window_left, int64_t window_right,
                float dropout_p, uint64_t dropout_seed, hipStream_t st) {
   if (!fill_dropout(p.drop, dropout_p, dropout_seed))
-    return fail(FA_ERR_INVALID, "%s: dropout_p must be in [0, 1)", name);
+    return fail(FA_ERR_INVALID, "%s: dropout_p must be in [0, 1 - 2^-17]", name);
   p.scale = softmax_scale;
   p.scale_log2 = softmax_scale * fa::kLog2e;
   p.softcap = softcap;
@@ -204,6 +209,8 @@ int bwd_check_common(const char* name, const void* q, const void* k, const void*
 }
 
 }  // namespace
+
+int fa_set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
@@ -265,7 +272,7 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
     p.bias_sq = bias_stride[2]; p.bias_sk = bias_stride[3];
   }
   if (!fill_dropout(p.drop, dropout_p, dropout_seed))
-    return fail(FA_ERR_INVALID, "fa_fwd_dense: dropout_p must be in [0, 1)");
+    return fail(FA_ERR_INVALID, "fa_fwd_dense: dropout_p must be in [0, 1 - 2^-17]");
   p.num_splits = 1;
   p.heavy_first = p.causal || p.window_right >= 0;
   return hip_status(launch_fwd(dtype, p, fa::kModePrefill, (int)head_dim,
@@ -283,12 +290,15 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   int64_t alibi_batch_stride, const int32_t* seqused_q,
                   const int32_t* seqused_k, const int32_t* cu_seqlens_out,
                   const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
-                  float dropout_p, uint64_t dropout_seed, fa_stream_t stream) {
+                  int64_t num_pages, int64_t block_table_cols, float dropout_p,
+                  uint64_t dropout_seed, fa_stream_t stream) {
   if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k || !q_stride || !k_stride ||
       !v_stride || !o_stride)
     return fail(FA_ERR_INVALID, "fa_fwd_varlen: null pointer argument");
-  if (block_table && page_size <= 0)
-    return fail(FA_ERR_INVALID, "fa_fwd_varlen: page_size must be positive with a block table");
+  if (block_table && (page_size <= 0 || num_pages <= 0 || block_table_cols <= 0 ||
+                      num_pages > INT32_MAX || block_table_cols > INT32_MAX))
+    return fail(FA_ERR_INVALID, "fa_fwd_varlen: a block table needs positive page_size, "
+                                "num_pages and block_table_cols");
   if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_varlen: lse without lse_stride");
   if (!supported_dtype(dtype))
     return fail(FA_ERR_UNSUPPORTED, "fa_fwd_varlen: dtype %d not supported", dtype);
@@ -314,6 +324,7 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
     p.k_sb = k_stride[0]; p.k_ss = k_stride[1]; p.k_sh = k_stride[2];
     p.v_sb = v_stride[0]; p.v_ss = v_stride[1]; p.v_sh = v_stride[2];
     p.block_table = block_table; p.bt_stride = block_table_stride; p.page_size = (int)page_size;
+    p.cache_blocks = (int)num_pages; p.bt_cols = (int)block_table_cols;
   } else {
     p.k_ss = k_stride[0]; p.k_sh = k_stride[1];
     p.v_ss = v_stride[0]; p.v_sh = v_stride[1];
@@ -323,7 +334,7 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
   p.cu_q = cu_seqlens_q; p.cu_k = cu_seqlens_k;
   p.seqused_q = seqused_q; p.seqused_k = seqused_k; p.cu_o = cu_seqlens_out;
   if (!fill_dropout(p.drop, dropout_p, dropout_seed))
-    return fail(FA_ERR_INVALID, "fa_fwd_varlen: dropout_p must be in [0, 1)");
+    return fail(FA_ERR_INVALID, "fa_fwd_varlen: dropout_p must be in [0, 1 - 2^-17]");
   p.batch = (int)batch; p.seqlen_q = (int)max_seqlen_q; p.seqlen_k = (int)max_seqlen_k;
   p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
   fill_scale(p, softmax_scale, softcap, alibi_slopes);
@@ -454,9 +465,15 @@ int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_
   return FA_OK;
 }
 
-int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void* out,
-                   float* lse, const int32_t* cache_seqlens, const int32_t* block_table,
-                   int64_t block_table_stride, int64_t page_size, const int32_t* cache_batch_idx,
+}  // extern "C"
+
+// fa_fwd_kvcache and fa_fwd_kvcache_noalloc: argument checks, then the split
+// and combine launches.  `workspace` holds the split partials (checked
+// against the plan here); `name` prefixes every error message.
+int fa_kvcache_run(const char* name, const void* q, const void* k_cache, const void* v_cache,
+                   void* out, float* lse, const int32_t* cache_seqlens,
+                   const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
+                   int64_t cache_blocks, const int32_t* cache_batch_idx,
                    const int32_t* cache_leftpad, int64_t batch, int64_t seqlen_q,
                    int64_t max_keys, int64_t heads_q, int64_t heads_k, int64_t head_dim,
                    const int64_t* q_stride, const int64_t* k_cache_stride,
@@ -467,34 +484,34 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
                    int64_t workspace_bytes, fa_stream_t stream) {
   if (!q || !k_cache || !v_cache || !out || !q_stride || !k_cache_stride || !v_cache_stride ||
       !o_stride)
-    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: null pointer argument");
-  if (lse && !lse_stride) return fail(FA_ERR_INVALID, "fa_fwd_kvcache: lse without lse_stride");
+    return fail(FA_ERR_INVALID, "%s: null pointer argument", name);
+  if (lse && !lse_stride) return fail(FA_ERR_INVALID, "%s: lse without lse_stride", name);
   if (!supported_dtype(dtype))
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: dtype %d not supported", dtype);
+    return fail(FA_ERR_UNSUPPORTED, "%s: dtype %d not supported", name, dtype);
   if (!supported_head_dim(head_dim))
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: head_dim %lld not supported",
+    return fail(FA_ERR_UNSUPPORTED, "%s: head_dim %lld not supported", name,
                 (long long)head_dim);
   if (batch < 0 || seqlen_q < 0 || max_keys < 0 || heads_q <= 0 || heads_k <= 0 ||
-      heads_q % heads_k != 0)
-    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: bad sizes");
+      heads_q % heads_k != 0 || cache_blocks < 0 || cache_blocks > INT32_MAX)
+    return fail(FA_ERR_INVALID, "%s: bad sizes", name);
   if (block_table && page_size <= 0)
-    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: page_size must be positive");
+    return fail(FA_ERR_INVALID, "%s: page_size must be positive", name);
   if (seqlen_q * (heads_q / heads_k) > kMaxLen || max_keys > kMaxLen)
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: sizes exceed 2^29");
+    return fail(FA_ERR_UNSUPPORTED, "%s: sizes exceed 2^29", name);
   const int64_t eb = elem_bytes(dtype);
   if (!aligned16(q, q_stride, 3, eb) || !aligned16(k_cache, k_cache_stride, 3, eb) ||
       !aligned16(v_cache, v_cache_stride, 3, eb) || !aligned16(out, o_stride, 3, eb))
-    return fail(FA_ERR_UNSUPPORTED, "fa_fwd_kvcache: tensors must be 16-byte aligned with "
-                                    "strides that are multiples of 16 bytes");
+    return fail(FA_ERR_UNSUPPORTED, "%s: tensors must be 16-byte aligned with "
+                                    "strides that are multiples of 16 bytes", name);
   const KvPlan plan = kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
                                    block_table ? page_size : 0);
   if (num_splits != plan.num_splits)
-    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: num_splits %d does not match the plan (%d)",
+    return fail(FA_ERR_INVALID, "%s: num_splits %d does not match the plan (%d)", name,
                 (int)num_splits, plan.num_splits);
   if (plan.num_splits > 1 &&
       (!workspace || workspace_bytes < plan.o_part_bytes + plan.lse_part_bytes ||
        reinterpret_cast<uintptr_t>(workspace) % 16 != 0))
-    return fail(FA_ERR_INVALID, "fa_fwd_kvcache: workspace too small or misaligned (%lld < %lld)",
+    return fail(FA_ERR_INVALID, "%s: workspace too small or misaligned (%lld < %lld)", name,
                 (long long)workspace_bytes, (long long)(plan.o_part_bytes + plan.lse_part_bytes));
   if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
   // fp32 runs every key of a row in one workgroup: the plan's split count is
@@ -511,6 +528,7 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     d.seqlens = cache_seqlens;
     d.block_table = block_table; d.bt_stride = block_table_stride; d.page_size = (int)page_size;
     d.cache_rows = cache_batch_idx; d.leftpad = cache_leftpad;
+    d.cache_blocks = (int)cache_blocks;
     d.batch = (int)batch; d.seqlen_q = (int)seqlen_q; d.heads_q = (int)heads_q;
     d.heads_k = (int)heads_k; d.group = (int)(heads_q / heads_k); d.max_keys = (int)max_keys;
     d.scale = softmax_scale; d.scale_log2 = softmax_scale * fa::kLog2e;
@@ -525,7 +543,7 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     }
     const bool generic = alibi_slopes != nullptr || !(softmax_scale > 0.f);
     return hip_status(fa_launch_decode(dtype, d, (int)head_dim, generic, (hipStream_t)stream),
-                      "fa_fwd_kvcache decode launch");
+                      name);
   }
   fa::FwdParams p{};
   p.q = q; p.k = k_cache; p.v = v_cache; p.o = out; p.lse = lse;
@@ -545,6 +563,7 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
   p.seqlens_k = cache_seqlens;
   p.block_table = block_table; p.bt_stride = block_table_stride; p.page_size = (int)page_size;
   p.cache_rows = cache_batch_idx; p.leftpad = cache_leftpad;
+  p.cache_blocks = (int)cache_blocks;
   p.num_splits = f32 ? 1 : plan.num_splits; p.split_tiles = plan.split_tiles;
   if (p.num_splits > 1) {
     p.o_part = static_cast<float*>(workspace);
@@ -557,7 +576,29 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
     e = fa_launch_combine(dtype, p.o_part, p.lse_part, out, lse, plan.num_splits, (int)batch,
                           (int)seqlen_q, (int)heads_q, (int)head_dim, o_stride, lse_stride,
                           (hipStream_t)stream);
-  return hip_status(e, "fa_fwd_kvcache launch");
+  return hip_status(e, name);
+}
+
+extern "C" {
+
+int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void* out,
+                   float* lse, const int32_t* cache_seqlens, const int32_t* block_table,
+                   int64_t block_table_stride, int64_t page_size, int64_t cache_blocks,
+                   const int32_t* cache_batch_idx, const int32_t* cache_leftpad, int64_t batch,
+                   int64_t seqlen_q, int64_t max_keys, int64_t heads_q, int64_t heads_k,
+                   int64_t head_dim, const int64_t* q_stride, const int64_t* k_cache_stride,
+                   const int64_t* v_cache_stride, const int64_t* o_stride,
+                   const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
+                   int64_t window_left, int64_t window_right, const float* alibi_slopes,
+                   int64_t alibi_batch_stride, int32_t num_splits, void* workspace,
+                   int64_t workspace_bytes, fa_stream_t stream) {
+  return fa_kvcache_run("fa_fwd_kvcache", q, k_cache, v_cache, out, lse, cache_seqlens,
+                        block_table, block_table_stride, page_size, cache_blocks,
+                        cache_batch_idx, cache_leftpad, batch, seqlen_q, max_keys, heads_q,
+                        heads_k, head_dim, q_stride, k_cache_stride, v_cache_stride, o_stride,
+                        lse_stride, dtype, softmax_scale, causal, window_left, window_right,
+                        alibi_slopes, alibi_batch_stride, num_splits, workspace,
+                        workspace_bytes, stream);
 }
 
 int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, float* lse_out,
@@ -610,7 +651,7 @@ int fa_attn_probs(const void* q, const void* k, const float* lse, float* probs, 
   p.window_left = clamp_window(window_left);
   p.window_right = clamp_window(window_right);
   if (!fill_dropout(p.drop, dropout_p, dropout_seed))
-    return fail(FA_ERR_INVALID, "fa_attn_probs: dropout_p must be in [0, 1)");
+    return fail(FA_ERR_INVALID, "fa_attn_probs: dropout_p must be in [0, 1 - 2^-17]");
   return hip_status(fa_launch_probs(dtype, p, (hipStream_t)stream), "fa_attn_probs launch");
 }
 

@@ -539,8 +539,11 @@ void bwd_dkdv_kernel(const BwdParams p) {
     if (wl >= 0) need = need || p1 - wl > wk0;
     return need;
   };
-  auto head_of = [&](int it) { return kvh * p.group + it / NM; };
-  auto m0_of = [&](int it) { return (m_begin + it % NM) * BM; };
+  // Divisor for the work-item split below: NM is 0 for key blocks no query
+  // row sees (J = 0), where only the empty prologue loads call these.
+  const int NMd = NM > 0 ? NM : 1;
+  auto head_of = [&](int it) { return kvh * p.group + it / NMd; };
+  auto m0_of = [&](int it) { return (m_begin + it % NMd) * BM; };
 
   // ------------------------------------------------------------ DMA stream
   // Waves [0, NW/2) copy Q tiles, the others dO tiles; each wave writes
@@ -633,7 +636,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
     const float* Es = reinterpret_cast<const float*>(smem_b + 2 * NS * TILEB + (NS + stage) * FB);
     const int hq = head_of(it), m0 = m0_of(it);
     float slope = 0.f;
-    if (GENERIC && p.alibi != nullptr) slope = slopes_lds[it / NM];
+    if (GENERIC && p.alibi != nullptr) slope = slopes_lds[it / NMd];
     f32x16 s[NRB], dp[NRB];
     const uint8_t* Qb = reinterpret_cast<const uint8_t*>(Qs);
     const uint8_t* Db = reinterpret_cast<const uint8_t*>(Ds);

@@ -17,15 +17,6 @@ template <int D> struct BwdCfg {
   static constexpr int KV_NW = 4, KV_BM = D >= 128 ? 32 : 64, KV_NS = 3, KV_WPE = 1;
 };
 
-template <class Kern>
-hipError_t set_lds(Kern kern, int bytes, bool& done) {
-  if (done) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess) done = true;
-  return e;
-}
-
 template <class T, int D, bool GEN, int PASS, bool VARLEN>
 hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
@@ -34,8 +25,8 @@ hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   // The ALiBi slope table (one float per query head of the group) follows the
   // stages; the attribute allows the largest table that still fits.
   constexpr int kMaxLds = 160 * 1024;
-  static bool lds_set = false;
-  hipError_t e = set_lds(kern, kMaxLds, lds_set);
+  static std::atomic<uint64_t> lds_devices{0};
+  hipError_t e = set_lds_limit(lds_devices, kern, kMaxLds);
   if (e != hipSuccess) return e;
   const int64_t lds = Tile::LDS_BYTES + (GEN && p.alibi != nullptr ? 4 * (int64_t)p.group : 0);
   if (lds > kMaxLds) return hipErrorInvalidConfiguration;
@@ -54,8 +45,8 @@ hipError_t launch_bwd_v(BwdParams p, hipStream_t st) {
   {
     using Tile = BwdDqTile<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS>;
     auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS, GEN, C::DQ_WPE, VARLEN>;
-    static bool lds_set = false;
-    hipError_t e = set_lds(kern, Tile::LDS_BYTES, lds_set);
+    static std::atomic<uint64_t> lds_devices{0};
+    hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES);
     if (e != hipSuccess) return e;
     p.n_blocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
     const int64_t total = (int64_t)p.n_blocks * p.heads_q * p.batch;

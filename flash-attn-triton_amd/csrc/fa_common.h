@@ -9,7 +9,27 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace fa {
+
+// Raises a kernel's dynamic-LDS limit to `bytes` on the current device, once
+// per device: the attribute is device state, so a process that launches on
+// several devices sets it on each.  `devices` is one bit per device
+// (devices 0..63; others set it on every call), a static of the call site;
+// concurrent first calls both set the attribute, which is harmless.
+template <class Kern>
+inline hipError_t set_lds_limit(std::atomic<uint64_t>& devices, Kern kern, int bytes) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = dev >= 0 && dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit != 0 && (devices.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+  e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit != 0) devices.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -271,7 +291,8 @@ __device__ inline u32x4 philox4x32_10(u32x4 c, uint32_t k0, uint32_t k1) {
 // Dropout mask.  Element (batch b, query head h, query row i, key j; rows and
 // keys local to the sequence) keeps its probability iff its 16-bit draw is at
 // least t16 = round(p * 65536), and a kept probability is scaled by
-// 1 / (1 - p).  The draws come 8 to a Philox call: call
+// 65536 / (65536 - t16), the reciprocal of the keep probability (an unbiased
+// mask).  The draws come 8 to a Philox call: call
 // (2 (j / 16) + (j / 4) % 2, i, h, b) under key (seed_lo, seed_hi) covers the
 // keys 16 (j / 16) + 4 s + {0, 1, 2, 3, 8, 9, 10, 11} (s = (j / 4) % 2) in the
 // order of its eight 16-bit halves, word e / 2 bits 16 (e % 2).  That is the
@@ -281,7 +302,7 @@ struct DropoutCfg {
   int enabled;
   uint32_t seed_lo, seed_hi;
   int t16;          // keep iff draw >= t16 (0 .. 65536)
-  float scale;      // 1 / (1 - p)
+  float scale;      // 65536 / (65536 - t16)
 };
 
 // Draws for keys 16 G + 4 s + {0..3, 8..11} of one row (one call).

@@ -83,7 +83,8 @@ void decode_kernel(const DecodeParams p) {
   const int b = id % p.batch;
   const int split = id / p.batch;
 
-  const int L = p.seqlens != nullptr ? p.seqlens[b] : p.max_keys;
+  int crow, lpad;
+  const int L = decode_keys(p, b, &crow, &lpad);
   const int k_begin = split * p.split_keys;
   // Splits past the cache end hold no keys (the combine skips them).  Split
   // 0 always runs, so that an empty cache still writes its rows (0 and LSE
@@ -123,24 +124,26 @@ void decode_kernel(const DecodeParams p) {
   // batched caches at slot leftpad + j of cache row cache_rows[b].
   const int* bt_row = p.block_table != nullptr ? p.block_table + (int64_t)b * p.bt_stride : nullptr;
   int64_t row_k0 = 0, row_v0 = 0;
-  if (bt_row == nullptr) {
-    const int crow = p.cache_rows != nullptr ? p.cache_rows[b] : b;
-    const int lp = p.leftpad != nullptr ? p.leftpad[b] : 0;
-    row_k0 = (int64_t)crow * p.k_sb + (int64_t)lp * p.k_ss;
-    row_v0 = (int64_t)crow * p.v_sb + (int64_t)lp * p.v_ss;
+  if (bt_row == nullptr && L > 0) {
+    row_k0 = (int64_t)crow * p.k_sb + (int64_t)lpad * p.k_ss;
+    row_v0 = (int64_t)crow * p.v_sb + (int64_t)lpad * p.v_ss;
   }
   row_k0 += (int64_t)kvh * p.k_sh;
   row_v0 += (int64_t)kvh * p.v_sh;
   // Offsets of the first key of the tile starting at n0 (a tile never
-  // straddles a page: the host only routes page_size % 32 == 0 here).
+  // straddles a page: the host only routes page_size % 32 == 0 here), or -1
+  // when the block table names a page outside the cache: that tile reads as
+  // zeros (an empty buffer resource) instead of leaving the cache.
   auto tile_k = [&](int n0) -> int64_t {
     if (bt_row == nullptr) return row_k0 + (int64_t)n0 * p.k_ss;
     const int page = bt_row[n0 / p.page_size];
+    if (page < 0 || page >= p.cache_blocks) return -1;
     return row_k0 + (int64_t)page * p.k_sb + (int64_t)(n0 % p.page_size) * p.k_ss;
   };
   auto tile_v = [&](int n0) -> int64_t {
     if (bt_row == nullptr) return row_v0 + (int64_t)n0 * p.v_ss;
     const int page = bt_row[n0 / p.page_size];
+    if (page < 0 || page >= p.cache_blocks) return -1;
     return row_v0 + (int64_t)page * p.v_sb + (int64_t)(n0 % p.page_size) * p.v_ss;
   };
 
@@ -175,8 +178,9 @@ void decode_kernel(const DecodeParams p) {
   // path, so each wait names only the tile it needs.
   auto load_k = [&](int tt, u32x4* kr_) {
     const int n0 = k_begin + tt * BN;
-    const bool live = n0 < k_end;
-    const auto rs = make_rsrc(live ? kg + tile_k(n0) : kg,
+    const int64_t off = n0 < k_end ? tile_k(n0) : -1;
+    const bool live = off >= 0;
+    const auto rs = make_rsrc(live ? kg + off : kg,
                               live ? rows_extent(0, L - n0, p.k_ss, D) : 0u);
 #pragma unroll
     for (int m = 0; m < VCH; ++m)
@@ -185,8 +189,9 @@ void decode_kernel(const DecodeParams p) {
   u32x4 vreg[VCH];
   auto load_v = [&](int tt) {
     const int n0 = k_begin + tt * BN;
-    const bool live = n0 < k_end;
-    const auto rs = make_rsrc(live ? vg + tile_v(n0) : vg,
+    const int64_t off = n0 < k_end ? tile_v(n0) : -1;
+    const bool live = off >= 0;
+    const auto rs = make_rsrc(live ? vg + off : vg,
                               live ? rows_extent(0, L - n0, p.v_ss, D) : 0u);
 #pragma unroll
     for (int m = 0; m < VCH; ++m)
@@ -385,7 +390,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(const DecodeParams 
   const int h = (int)(row % p.heads_q);
   const int i = (int)((row / p.heads_q) % p.seqlen_q);
   const int b = (int)(row / ((int64_t)p.heads_q * p.seqlen_q));
-  const int L = p.seqlens != nullptr ? p.seqlens[b] : p.max_keys;
+  const int L = decode_keys(p, b, nullptr, nullptr);
   const int n = min(p.num_splits, (L + p.split_keys - 1) / p.split_keys);
   // Running (max, sum, weighted rows) over batches of splits.
   float m = -INFINITY, tot = 0.f;
@@ -431,13 +436,8 @@ template <class T, int D, bool GEN>
 hipError_t launch_decode_t(const DecodeParams& p, hipStream_t st) {
   using Tile = DecodeTile<D>;
   auto kern = decode_kernel<T, D, GEN>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   const int64_t wgs = (int64_t)p.num_splits * p.heads_k * p.batch;
   if (wgs <= 0) return hipSuccess;
   if (wgs > 0x7fffffff) return hipErrorInvalidConfiguration;

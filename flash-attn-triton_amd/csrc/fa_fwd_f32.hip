@@ -97,6 +97,7 @@ void fwd_f32_kernel(const FwdParams p) {
       lse_base = (int64_t)os * p.lse_ss;
       if (p.block_table != nullptr) {
         bt_row = p.block_table + (int64_t)b * p.bt_stride;   // paged varlen
+        if (p.bt_cols > 0) Sk = min(Sk, (int)min((int64_t)p.bt_cols * p.page_size, (int64_t)1 << 30));
       } else {
         k_base = (int64_t)ks * p.k_ss;
         v_base = (int64_t)ks * p.v_ss;
@@ -119,18 +120,23 @@ void fwd_f32_kernel(const FwdParams p) {
     Sq = p.seqlen_q;
     Sk = p.seqlen_k;
     if (p.seqlens_k != nullptr) Sk = p.seqlens_k[b];
-    if (p.kv_causal_offset) qoff = (int64_t)Sk - Sq;
-    q_base = (int64_t)b * p.q_sb;
-    o_base = (int64_t)b * p.o_sb;
-    lse_base = (int64_t)b * p.lse_sb;
+    // Keys within the cache (see FwdParams::cache_blocks).
+    int lp = 0;
     if (p.block_table != nullptr) {
       bt_row = p.block_table + (int64_t)b * p.bt_stride;
     } else {
       const int row = p.cache_rows != nullptr ? p.cache_rows[b] : b;
-      const int lp = p.leftpad != nullptr ? p.leftpad[b] : 0;
+      lp = p.leftpad != nullptr ? p.leftpad[b] : 0;
+      lp = max(0, min(lp, p.seqlen_k));
+      if (row < 0 || row >= p.cache_blocks) Sk = 0;
       k_base = (int64_t)row * p.k_sb + (int64_t)lp * p.k_ss;
       v_base = (int64_t)row * p.v_sb + (int64_t)lp * p.v_ss;
     }
+    Sk = max(0, min(Sk, p.seqlen_k - lp));
+    if (p.kv_causal_offset) qoff = (int64_t)Sk - Sq;
+    q_base = (int64_t)b * p.q_sb;
+    o_base = (int64_t)b * p.o_sb;
+    lse_base = (int64_t)b * p.lse_sb;
   }
   k_base += (int64_t)kvh * p.k_sh;
   v_base += (int64_t)kvh * p.v_sh;
@@ -183,9 +189,12 @@ void fwd_f32_kernel(const FwdParams p) {
     }
   }
 
+  // Element offset of key j's row, or -1 for a page outside the cache (the
+  // key then reads as zeros).
   auto key_offset = [&](int j, int64_t base, int64_t sb, int64_t ss) -> int64_t {
     if (bt_row != nullptr) {
       const int page = bt_row[j / p.page_size];
+      if (page < 0 || page >= p.cache_blocks) return -1;
       return base + (int64_t)page * sb + (int64_t)(j % p.page_size) * ss;
     }
     return base + (int64_t)j * ss;
@@ -213,8 +222,10 @@ void fwd_f32_kernel(const FwdParams p) {
         const int j = n0 + n;
         f32x4 kx = {0.f, 0.f, 0.f, 0.f}, vx = {0.f, 0.f, 0.f, 0.f};
         if (j < Sk) {
-          kx = *reinterpret_cast<const f32x4*>(kg + key_offset(j, k_base, p.k_sb, p.k_ss) + d);
-          vx = *reinterpret_cast<const f32x4*>(vg + key_offset(j, v_base, p.v_sb, p.v_ss) + d);
+          const int64_t ko = key_offset(j, k_base, p.k_sb, p.k_ss);
+          const int64_t vo = key_offset(j, v_base, p.v_sb, p.v_ss);
+          if (ko >= 0) kx = *reinterpret_cast<const f32x4*>(kg + ko + d);
+          if (vo >= 0) vx = *reinterpret_cast<const f32x4*>(vg + vo + d);
         }
         *reinterpret_cast<f32x4*>(Ks + n * KSTR + d) = kx;
         *reinterpret_cast<f32x4*>(Vs + n * VSTR + d) = vx;
@@ -313,13 +324,8 @@ template <int D, int MODE, bool GEN>
 hipError_t launch_f32_d(FwdParams p, hipStream_t st) {
   using Tile = F32Tile<D>;
   auto kern = fwd_f32_kernel<D, MODE, GEN>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   const int rows = MODE == kModePrefill ? p.seqlen_q : p.seqlen_q * p.group;
   p.n_mblocks = (rows + Tile::BM - 1) / Tile::BM;
   const int64_t outer = (int64_t)(MODE == kModePrefill ? p.heads_q : p.heads_k) * p.batch;

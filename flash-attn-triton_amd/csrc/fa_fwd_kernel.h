@@ -66,6 +66,11 @@ struct FwdParams {
   const int* seqused_q; const int* seqused_k; const int* cu_o;
   const int* seqlens_k;
   const int* block_table; int64_t bt_stride; int page_size;
+  // Leading extent of a paged / batched cache (pages or cache rows) and the
+  // block table's columns (0: bounded by seqlen_k): pages outside the cache
+  // read as zeros and key counts are clamped to what the table and the cache
+  // hold, so no read leaves them whatever the device arrays contain.
+  int cache_blocks, bt_cols;
   const int* cache_rows;
   const int* leftpad;
   int kv_causal_offset;
@@ -159,6 +164,7 @@ void fwd_kernel(const FwdParams p) {
         // Paged varlen: key j of sequence b is slot j % page_size of page
         // block_table[b][j / page_size].
         bt_row = p.block_table + (int64_t)b * p.bt_stride;
+        if (p.bt_cols > 0) Sk = min(Sk, (int)min((int64_t)p.bt_cols * p.page_size, (int64_t)1 << 30));
       } else {
         k_base = (int64_t)ks * p.k_ss;
         v_base = (int64_t)ks * p.v_ss;
@@ -181,18 +187,25 @@ void fwd_kernel(const FwdParams p) {
     Sq = p.seqlen_q;
     Sk = p.seqlen_k;
     if (p.seqlens_k != nullptr) Sk = p.seqlens_k[b];
-    if (p.kv_causal_offset) qoff = (int64_t)Sk - Sq;
-    q_base = (int64_t)b * p.q_sb;
-    o_base = (int64_t)b * p.o_sb;
-    lse_base = (int64_t)b * p.lse_sb;
+    // Keys within the cache: seqlen_k (the capacity, for a paged cache at
+    // most the table's columns times page_size) less the left padding; a
+    // batched-cache row outside the cache holds none.
+    int lp = 0;
     if (p.block_table != nullptr) {
       bt_row = p.block_table + (int64_t)b * p.bt_stride;
     } else {
       const int row = p.cache_rows != nullptr ? p.cache_rows[b] : b;
-      const int lp = p.leftpad != nullptr ? p.leftpad[b] : 0;
+      lp = p.leftpad != nullptr ? p.leftpad[b] : 0;
+      lp = max(0, min(lp, p.seqlen_k));
+      if (row < 0 || row >= p.cache_blocks) Sk = 0;
       k_base = (int64_t)row * p.k_sb + (int64_t)lp * p.k_ss;
       v_base = (int64_t)row * p.v_sb + (int64_t)lp * p.v_ss;
     }
+    Sk = max(0, min(Sk, p.seqlen_k - lp));
+    if (p.kv_causal_offset) qoff = (int64_t)Sk - Sq;
+    q_base = (int64_t)b * p.q_sb;
+    o_base = (int64_t)b * p.o_sb;
+    lse_base = (int64_t)b * p.lse_sb;
   }
   k_base += (int64_t)kvh * p.k_sh;
   v_base += (int64_t)kvh * p.v_sh;
@@ -252,9 +265,12 @@ void fwd_kernel(const FwdParams p) {
   }
 
   // ---------------------------------------------------------------- tile I/O
+  // Element offset of key j's row, or -1 for a page outside the cache (the
+  // key then reads as zeros).
   auto key_offset = [&](int j, int64_t base, int64_t sb, int64_t ss) -> int64_t {
     if (bt_row != nullptr) {
       const int page = bt_row[j / p.page_size];
+      if (page < 0 || page >= p.cache_blocks) return -1;
       return base + (int64_t)page * sb + (int64_t)(j % p.page_size) * ss;
     }
     return base + (int64_t)j * ss;
@@ -271,7 +287,10 @@ void fwd_kernel(const FwdParams p) {
       if (c < KCH) {
         const int n = c / CPR, d = (c % CPR) * 8;
         const int j = n0 + n;
-        if (j < Sk && d < D) kreg[i] = load16(kg + key_offset(j, k_base, p.k_sb, p.k_ss) + d);
+        if (j < Sk && d < D) {
+          const int64_t off = key_offset(j, k_base, p.k_sb, p.k_ss);
+          if (off >= 0) kreg[i] = load16(kg + off + d);
+        }
       }
     }
 #pragma unroll
@@ -284,7 +303,10 @@ void fwd_kernel(const FwdParams p) {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int j = n0 + ng * 4 + u;
-          if (j < Sk && d < D) vreg[i][u] = load16(vg + key_offset(j, v_base, p.v_sb, p.v_ss) + d);
+          if (j < Sk && d < D) {
+            const int64_t off = key_offset(j, v_base, p.v_sb, p.v_ss);
+            if (off >= 0) vreg[i][u] = load16(vg + off + d);
+          }
         }
       }
     }

@@ -21,13 +21,8 @@ template <class T, int D, int NW, int BN, int MODE, bool GEN>
 hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipStream_t st) {
   using Tile = FwdTile<D, NW, BN>;
   auto kern = fwd_kernel<T, D, NW, BN, MODE, GEN>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   p.n_mblocks = (rows_for_grid + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * outer_blocks;
   if (total <= 0) return hipSuccess;
@@ -50,13 +45,8 @@ template <class T, int D, int NW, int BN, bool GEN, int WPE, bool BIAS = false>
 hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
   using Tile = PrefillTile<D, NW, BN>;
   auto kern = prefill_kernel<T, D, NW, BN, GEN, WPE, BIAS>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   p.n_mblocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * p.heads_q * p.batch;
   if (total <= 0) return hipSuccess;
@@ -71,13 +61,8 @@ template <class T, int D, bool VARLEN>
 hipError_t launch_prefill_pp(FwdParams p, hipStream_t st) {
   using Tile = PingPongTile<D>;
   auto kern = prefill_pp_kernel<T, D, VARLEN>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   p.n_mblocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * p.heads_q * p.batch;
   if (total <= 0) return hipSuccess;

@@ -371,13 +371,8 @@ template <int D, int NW, int BN, int WPE>
 hipError_t launch_int8_cfg(Int8Params p, hipStream_t st) {
   using Tile = Int8Tile<D, NW, BN>;
   auto kern = int8_fwd_kernel<D, NW, BN, WPE>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   p.n_mblocks = (p.seqlen + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * p.batch * p.heads;
   if (total <= 0) return hipSuccess;
@@ -392,13 +387,8 @@ template <int D>
 hipError_t launch_int8_pp(Int8Params p, hipStream_t st) {
   using Tile = Int8PingPongTile<D>;
   auto kern = int8_pp_kernel<D>;
-  static bool lds_attr_set = false;
-  if (!lds_attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, Tile::LDS_BYTES);
-    if (e != hipSuccess) return e;
-    lds_attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_devices{0};
+  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
   p.n_mblocks = (p.seqlen + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * p.batch * p.heads;
   if (total <= 0) return hipSuccess;

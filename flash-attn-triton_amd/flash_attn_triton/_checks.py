@@ -64,11 +64,21 @@ class Deferred:
         self.flush()
         raise exc
 
-    def flush(self) -> list:
-        """Raise the first failing queued check; return the queued values."""
+    def flush(self, launch=None) -> list:
+        """Raise the first failing queued check; return the queued values.
+
+        With ``launch`` (a callable that enqueues kernels on the current
+        stream), the queued scalars are copied to pinned host memory first,
+        ``launch()`` runs, and only then does the host wait, for the copy
+        alone: the launched work runs while the host reads the checks, and
+        a failing check still raises before this call returns.  Only kernels
+        that stay inside their buffers whatever the checked arrays hold may be
+        launched this way."""
         items, self._items = self._items, []
         self._minmax = {}
         if not items:
+            if launch is not None:
+                launch()
             return []
         scalars, dtypes = [], []
         for it in items:
@@ -78,7 +88,17 @@ class Deferred:
                     s = s.to(torch.int32 if s.dtype == torch.bool else torch.int64)
                 scalars.append(s.view(torch.int32))
                 dtypes.append(s.dtype)
-        words = (torch.cat(scalars) if len(scalars) > 1 else scalars[0]).tolist()
+        packed = torch.cat(scalars) if len(scalars) > 1 else scalars[0]
+        if launch is None:
+            words = packed.tolist()
+        else:
+            host = torch.empty(packed.shape, dtype=packed.dtype, pin_memory=True)
+            host.copy_(packed, non_blocking=True)
+            done = torch.cuda.Event()
+            done.record()
+            launch()
+            done.synchronize()
+            words = host.tolist()
         host, pos = [], 0
         for dt in dtypes:
             n = _WORDS[dt]

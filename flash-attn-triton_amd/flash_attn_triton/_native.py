@@ -48,16 +48,17 @@ _SIGNATURES = {
                             _i64, _f32, _vp, _i64, _vp, _i64p, _f32, _u64, _vp]),
     "fa_fwd_varlen": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _i64p, _i64p, _int, _f32, _int, _i64,
-                             _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _f32, _u64,
-                             _vp]),
+                             _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                             _f32, _u64, _vp]),
     "fa_bwd_dense": (_int, [_vp] * 10 + [_i64] * 6 + [_i64p] * 9 +
                      [_int, _f32, _int, _i64, _i64, _i64, _f32, _vp, _i64, _f32, _u64, _vp]),
     "fa_bwd_varlen": (_int, [_vp] * 12 + [_i64] * 6 + [_i64p] * 9 +
                       [_int, _f32, _int, _i64, _i64, _f32, _vp, _i64, _f32, _u64, _vp]),
     "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
-    "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
-                              _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p, _i64p,
-                              _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64, _vp]),
+    "fa_fwd_kvcache": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp,
+                              _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p,
+                              _i64p, _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64,
+                              _vp]),
     "fa_attn_probs": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64, _i64,
                              _f32, _vp, _i64, _vp, _i64p, _f32, _u64, _vp]),
@@ -242,7 +243,9 @@ def fwd_varlen(q, k, v, out, lse, cu_q, cu_k, max_seqlen_q: int, max_seqlen_k: i
         int(window_left), int(window_right), float(softcap), _ptr(alibi),
         0 if alibi is None else int(alibi.stride(0)), _ptr(seqused_q), _ptr(seqused_k),
         _ptr(cu_out), _ptr(block_table), int(block_table.stride(0)) if paged else 0,
-        int(k.shape[1]) if paged else 0, float(dropout_p), int(dropout_seed), _stream(q.device))
+        int(k.shape[1]) if paged else 0, int(k.shape[0]) if paged else 0,
+        int(block_table.shape[1]) if paged else 0, float(dropout_p), int(dropout_seed),
+        _stream(q.device))
     _check(status, "fa_fwd_varlen")
 
 
@@ -273,7 +276,8 @@ def fwd_kvcache(q, k_cache, v_cache, out, lse, cache_seqlens, block_table, cache
     lse_stride = _strides(lse.stride()) if lse is not None else None
     status = lib.fa_fwd_kvcache(
         _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(lse), _ptr(cache_seqlens),
-        _ptr(block_table), int(bt_stride), int(page_size), _ptr(cache_batch_idx),
+        _ptr(block_table), int(bt_stride), int(page_size), int(k_cache.shape[0]),
+        _ptr(cache_batch_idx),
         _ptr(cache_leftpad), B, Sq, int(max_keys), Hq, Hk, D, _strides(q.stride()[:3]),
         _strides(k_cache.stride()[:3]), _strides(v_cache.stride()[:3]),
         _strides(out.stride()[:3]), lse_stride, dtype_code(q.dtype), float(softmax_scale),

@@ -451,10 +451,17 @@ def flash_attn_with_kvcache(
         alibi = _normalize_alibi(alibi_slopes, q.shape[0], q.shape[2], q.device)
     except ValueError as exc:
         chk.fail(exc)
-    alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
-    values = chk.flush()   # the one host synchronization of this call
-    if alibi is not None and not values[alibi_any]:
-        alibi = None
+    # Without an append, rotary or ALiBi slopes nothing the launch needs comes
+    # from the device checks, and the kernels keep every read inside the
+    # caches and the block table whatever cache_seqlens and block_table hold
+    # (fa_fwd_kvcache clamps them): the attention launch goes out before the
+    # host waits for the checks, which still raise before this call returns.
+    launch_first = n_new == 0 and cos_t is None and alibi is None
+    if not launch_first:
+        alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
+        values = chk.flush()   # the one host synchronization of this call
+        if alibi is not None and not values[alibi_any]:
+            alibi = None
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     from .triton_kernel.attention_kernel import _kernel_ready
@@ -475,10 +482,17 @@ def flash_attn_with_kvcache(
         qk = q_rot
     kc, vc = _kernel_ready(k_cache), _kernel_ready(v_cache)
     out = torch.empty(q.shape, dtype=q.dtype, device=q.device)
-    _native.fwd_kvcache(
-        qk, kc, vc, out, None, lengths32,
-        bt32, rows32, pads32,
-        int(cache_capacity), softmax_scale, causal, window_size[0], window_size[1], alibi)
+
+    def launch():
+        _native.fwd_kvcache(
+            qk, kc, vc, out, None, lengths32,
+            bt32, rows32, pads32,
+            int(cache_capacity), softmax_scale, causal, window_size[0], window_size[1], alibi)
+
+    if launch_first:
+        chk.flush(launch)   # the one host synchronization of this call
+    else:
+        launch()
     return _wrap_grad(out, q)
 
 

@@ -64,10 +64,13 @@ const char* fa_last_error_string(void);
  * natural-log logsumexp at lse[b*lse_stride[0] + h*lse_stride[1] +
  * i*lse_stride[2]]; rows with no visible key get out = 0 and lse = -inf.
  *
- * dropout_p in [0, 1) drops probabilities before the product with V
+ * dropout_p in [0, 1 - 2^-17] drops probabilities before the product with V
  * (attention_kernel.py:344-358): element (b, h, i, j) is kept iff its 16-bit
- * Philox4x32-10 draw under dropout_seed is >= round(p * 65536), and kept
- * values are scaled by 1 / (1 - p); the LSE is that of the undropped scores.
+ * Philox4x32-10 draw under dropout_seed is >= t16 = round(p * 65536), and kept
+ * values are scaled by 65536 / (65536 - t16), the reciprocal of the keep
+ * probability (1 / (1 - p) to within 2^-17 / (1 - p)), so the mask is
+ * unbiased; p < 2^-17 keeps everything.  The LSE is that of the undropped
+ * scores.
  * The draw of (b, h, i, j) is half j%4 + 4((j%16)/8) of the Philox call with
  * counter {2(j/16) + (j/4)%2, i, h, b} and key {seed, seed >> 32}; rows and
  * keys are local to the sequence (varlen: b is the sequence index).  The
@@ -104,7 +107,13 @@ int fa_fwd_dense(const void* q, const void* k, const void* v, void* out, float* 
  * with *_stride[3] = {page, slot, head}: key j of sequence b is slot
  * j % page_size of page block_table[b][j / page_size], the length of sequence
  * b still being cu_seqlens_k[b+1] - cu_seqlens_k[b] (paged varlen prefill,
- * flash_attn_interface.py:533-550, without the reference's gather).
+ * flash_attn_interface.py:533-550, without the reference's gather).  With a
+ * block table, num_pages is the caches' page count and block_table_cols the
+ * table's columns: a page index outside [0, num_pages) reads as zeros and a
+ * sequence's keys are clamped to block_table_cols * page_size, so no read
+ * leaves the caches or the table whatever the table holds (the Python layer
+ * rejects such tables first, flash_attn_interface.py:543-546).  cu_seqlens_*
+ * must describe rows inside q/k/v (they are not bounds-checked here).
  */
 int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float* lse,
                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t batch,
@@ -116,7 +125,8 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
                   int64_t alibi_batch_stride, const int32_t* seqused_q,
                   const int32_t* seqused_k, const int32_t* cu_seqlens_out,
                   const int32_t* block_table, int64_t block_table_stride, int64_t page_size,
-                  float dropout_p, uint64_t dropout_seed, fa_stream_t stream);
+                  int64_t num_pages, int64_t block_table_cols, float dropout_p,
+                  uint64_t dropout_seed, fa_stream_t stream);
 
 /* Backward of fa_fwd_dense: dq, dk, dv from dout.
  *
@@ -184,23 +194,29 @@ int fa_fwd_kvcache_plan(int64_t batch, int64_t seqlen_q, int64_t heads_q, int64_
  * split-KV launch plus a combine launch.
  *
  * q [B, Sq, Hq, D] (q_stride {batch, seq, head}); out likewise.
- * Paged (block_table != NULL): k_cache/v_cache [num_pages, page_size, Hk, D]
+ * Paged (block_table != NULL): k_cache/v_cache [cache_blocks, page_size, Hk, D]
  * with cache_stride {page, slot, head}; logical key t of sequence b lives in
  * page block_table[b*block_table_stride + t/page_size], slot t%page_size.
- * Batched (block_table == NULL): caches [rows, capacity, Hk, D] with
+ * Batched (block_table == NULL): caches [cache_blocks, capacity, Hk, D] with
  * cache_stride {row, slot, head}; sequence b reads cache row
  * cache_batch_idx[b] (nullable: b) from slot cache_leftpad[b] (nullable: 0).
  * cache_seqlens[b] (device int32, nullable: max_keys for every b) visible
- * keys.  When causal, query i sits at position i + L_b - Sq (bottom-right);
+ * keys.  max_keys is the capacity: the slots of a batched row, and for a
+ * paged cache at most the block table's columns times page_size.  Whatever
+ * the device arrays hold, no read leaves the caches or the table: lengths
+ * are clamped to [0, max_keys - leftpad], leftpad to [0, max_keys], and a
+ * page or cache row outside [0, cache_blocks) reads as zeros (a row: no keys).
+ * When causal, query i sits at position i + L_b - Sq (bottom-right);
  * otherwise at i.  window/alibi as fa_fwd_dense.  lse (nullable) is
  * [B, Hq, Sq] at lse[b*s0 + h*s1 + i*s2].  num_splits/workspace come from
  * fa_fwd_kvcache_plan (workspace may be NULL when its size is 0).
  */
 int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void* out,
                    float* lse, const int32_t* cache_seqlens, const int32_t* block_table,
-                   int64_t block_table_stride, int64_t page_size, const int32_t* cache_batch_idx,
-                   const int32_t* cache_leftpad, int64_t batch, int64_t seqlen_q,
-                   int64_t max_keys, int64_t heads_q, int64_t heads_k, int64_t head_dim,
+                   int64_t block_table_stride, int64_t page_size, int64_t cache_blocks,
+                   const int32_t* cache_batch_idx, const int32_t* cache_leftpad, int64_t batch,
+                   int64_t seqlen_q, int64_t max_keys, int64_t heads_q, int64_t heads_k,
+                   int64_t head_dim,
                    const int64_t* q_stride, const int64_t* k_cache_stride,
                    const int64_t* v_cache_stride, const int64_t* o_stride,
                    const int64_t* lse_stride, int dtype, float softmax_scale, int causal,

@@ -383,11 +383,40 @@ def test_dropout_keep_rate_and_scale(p):
     n = kept.size
     # Binomial: the kept fraction lies within 6 standard deviations of 1 - p.
     assert abs(kept.mean() - (1 - p)) < 6 * math.sqrt(p * (1 - p) / n)
-    np.testing.assert_allclose(f[kept], 1.0 / (1.0 - float(np.float32(p))), rtol=1e-15)
+    t16 = round(float(np.float32(p)) * 65536)
+    np.testing.assert_allclose(f[kept], 65536.0 / (65536 - t16), rtol=1e-15)
+    # The kept scale is within 2^-17 / (1 - p) of the reference's 1 / (1 - p).
+    assert abs(f[kept][0] * (1 - float(np.float32(p))) - 1) <= 2 ** -17 / (1 - p) + 1e-12
     # Every (batch, head) draws its own mask: masks of different heads agree
     # on about p^2 + (1-p)^2 of the elements, not on all of them.
     agree = (kept[0, 0] == kept[1, 3]).mean()
     assert abs(agree - (p * p + (1 - p) ** 2)) < 0.01
+
+
+@pytest.mark.parametrize("p", [1e-7, 2.0 ** -17, 3e-5, 0.25, 1 - 2.0 ** -12, 1 - 2.0 ** -16])
+def test_dropout_mask_is_unbiased(p):
+    # E[factor] = keep probability x kept scale must be exactly 1 for every
+    # p the 16-bit draws can express, including the extremes: p below
+    # 2^-17 keeps everything at scale 1, p = 1 - 2^-16 keeps one draw value
+    # in 65536 at scale 65536.
+    t16 = round(float(np.float32(p)) * 65536)
+    f = ora.dropout_factors(99, p, [0, 1, 2, 3], 8, 128, 256)
+    kept = f > 0
+    if t16 == 0:
+        np.testing.assert_array_equal(f, 1.0)
+        return
+    scale = f[kept].max() if kept.any() else 65536.0 / (65536 - t16)
+    np.testing.assert_array_equal(f[kept], scale)
+    assert scale * (65536 - t16) == 65536.0
+    # The kept fraction is the keep probability (binomial, 6 sigma).
+    q_keep = (65536 - t16) / 65536
+    n = f.size
+    assert abs(kept.mean() - q_keep) <= 6 * math.sqrt(q_keep * (1 - q_keep) / n) + 1.0 / n
+
+
+def test_dropout_rejects_p_that_keeps_nothing():
+    with pytest.raises(ValueError):
+        ora.dropout_factors(1, 1 - 2.0 ** -18, [0], 1, 4, 4)
 
 
 def test_dropout_mask_is_seed_dependent_and_p0_is_identity():
