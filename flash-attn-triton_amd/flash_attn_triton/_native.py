@@ -59,6 +59,10 @@ _SIGNATURES = {
                               _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p, _i64p,
                               _i64p, _int, _f32, _int, _i64, _i64, _vp, _i64, _i32, _vp, _i64,
                               _vp]),
+    "fa_fwd_kvcache_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp,
+                                      _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64p, _i64p,
+                                      _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64, _vp,
+                                      _i64, _vp]),
     "fa_attn_probs": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                              _i64, _i64p, _i64p, _i64p, _int, _f32, _int, _i64, _i64, _i64,
                              _f32, _vp, _i64, _vp, _i64p, _f32, _u64, _vp]),
@@ -285,6 +289,30 @@ def fwd_kvcache(q, k_cache, v_cache, out, lse, cache_seqlens, block_table, cache
         0 if alibi is None else int(alibi.stride(0)), splits, _ptr(workspace),
         int(ws_bytes), _stream(q.device))
     _check(status, "fa_fwd_kvcache")
+
+
+def fwd_kvcache_noalloc(q, k_cache, v_cache, out, lse, cache_seqlens, block_table,
+                        cache_batch_idx, cache_leftpad, max_keys: int, softmax_scale: float,
+                        causal: bool, window_left: int, window_right: int, alibi) -> None:
+    """fwd_kvcache through fa_fwd_kvcache_noalloc: the split partials live in
+    the library's per-GPU scratch array, so this call allocates nothing on the
+    device (calls that overlap on one GPU race; see the header)."""
+    lib = load()
+    B, Sq, Hq, D = q.shape
+    Hk = k_cache.shape[2]
+    page_size = k_cache.shape[1] if block_table is not None else 0
+    bt_stride = block_table.stride(0) if block_table is not None else 0
+    lse_stride = _strides(lse.stride()) if lse is not None else None
+    status = lib.fa_fwd_kvcache_noalloc(
+        _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(out), _ptr(lse), _ptr(cache_seqlens),
+        _ptr(block_table), int(bt_stride), int(page_size), int(k_cache.shape[0]),
+        _ptr(cache_batch_idx), _ptr(cache_leftpad), B, Sq, int(max_keys), Hq, Hk, D,
+        _strides(q.stride()[:3]), _strides(k_cache.stride()[:3]),
+        _strides(v_cache.stride()[:3]), _strides(out.stride()[:3]), lse_stride,
+        dtype_code(q.dtype), float(softmax_scale), int(bool(causal)), int(window_left),
+        int(window_right), _ptr(alibi), 0 if alibi is None else int(alibi.stride(0)),
+        _stream(q.device))
+    _check(status, "fa_fwd_kvcache_noalloc")
 
 
 def kvcache_append(k_new, v_new, k_cache, v_cache, cache_seqlens, block_table, cache_batch_idx,

@@ -224,6 +224,33 @@ int fa_fwd_kvcache(const void* q, const void* k_cache, const void* v_cache, void
                    int64_t alibi_batch_stride, int32_t num_splits, void* workspace,
                    int64_t workspace_bytes, fa_stream_t stream);
 
+/* fa_fwd_kvcache for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ *
+ * No counterpart in the reference (its KV-cache path is a Python loop).  The
+ * arguments are those of fa_fwd_kvcache without num_splits / workspace: the
+ * split-KV partials live in a device array inside the library, of
+ * FA_NOALLOC_SCRATCH_BYTES per GPU, held from the library's load until the
+ * process ends.  A call allocates nothing.  Shapes whose split workspace
+ * (fa_fwd_kvcache_plan's workspace_bytes) exceeds that size are rejected with
+ * FA_ERR_UNSUPPORTED before any launch.  All calls on one GPU share its
+ * array, which keeps the last call's contents: calls that overlap on one GPU
+ * (several streams or host threads) race and must be serialized by the
+ * caller.  Call with the stream's device current.
+ */
+#define FA_NOALLOC_SCRATCH_BYTES (16 << 20)
+int fa_fwd_kvcache_noalloc(const void* q, const void* k_cache, const void* v_cache, void* out,
+                           float* lse, const int32_t* cache_seqlens, const int32_t* block_table,
+                           int64_t block_table_stride, int64_t page_size, int64_t cache_blocks,
+                           const int32_t* cache_batch_idx, const int32_t* cache_leftpad,
+                           int64_t batch, int64_t seqlen_q, int64_t max_keys, int64_t heads_q,
+                           int64_t heads_k, int64_t head_dim, const int64_t* q_stride,
+                           const int64_t* k_cache_stride, const int64_t* v_cache_stride,
+                           const int64_t* o_stride, const int64_t* lse_stride, int dtype,
+                           float softmax_scale, int causal, int64_t window_left,
+                           int64_t window_right, const float* alibi_slopes,
+                           int64_t alibi_batch_stride, fa_stream_t stream);
+
 /* Materialized attention probabilities (return_attn_probs=True).
  *
  * Replaces the dense torch math of `_attention_with_probs`

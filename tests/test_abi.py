@@ -165,3 +165,17 @@ def test_varlen_cu_seqlens_errors_before_device_errors():
     with pytest.raises(ValueError, match="CUDA tensors"):
         flash_attn_varlen_func(q, q, q, torch.tensor([0, 4], dtype=torch.int32),
                                torch.tensor([0, 4], dtype=torch.int32), 4, 4)
+
+
+def test_noalloc_rejects_workspace_beyond_scratch_without_a_device(lib):
+    # The no-allocation KV-cache entry point checks the split workspace its
+    # plan needs against the fixed scratch array before touching any device.
+    st = _native._strides((4096, 4096, 128))
+    one = ctypes.c_void_p(16)   # never dereferenced: the size check fails first
+    args = (one, one, one, one, None, one, one, 32, 256, 64, None, None,
+            4096, 1, 8192, 32, 8, 128, st, st, st, st, None, 0, 0.088, 0, -1, -1, None, 0, None)
+    splits, ws = _native.kvcache_plan(4096, 1, 32, 8, 128, 8192, 256)
+    assert ws > (16 << 20)
+    status = lib.fa_fwd_kvcache_noalloc(*args)
+    assert status == _native.FA_ERR_UNSUPPORTED
+    assert b"scratch" in lib.fa_last_error_string()
