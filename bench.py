@@ -362,8 +362,8 @@ def make_copy(torch):
 # The dominant kernel(s) of each workload as rocprofv3 names them; the first
 # one is launched once per step.
 KERNELS = {
-    "dense_causal": ("fa::prefill_pp_kernel",),
-    "dense": ("fa::prefill_pp_kernel",),
+    "dense_causal": ("fa::prefill_persist_kernel",),
+    "dense": ("fa::prefill_persist_kernel",),
     "bwd_causal": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
     "bwd": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
     "int8_causal": ("fa::int8_pp_kernel",),

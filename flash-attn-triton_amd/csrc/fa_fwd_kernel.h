@@ -77,6 +77,8 @@ struct FwdParams {
   int num_splits, split_tiles;
   float* o_part; float* lse_part;
   int n_mblocks, total_blocks, heavy_first;
+  // prefill_persist_kernel: row blocks per workgroup.
+  int persist_rounds;
   // Dropout of the probabilities (prefill, GENERIC instantiations only).
   DropoutCfg drop;
 };

@@ -5,6 +5,7 @@
 
 #include "fa_prefill_kernel.h"
 #include "fa_prefill_pp.h"
+#include "fa_prefill_persist.h"
 
 namespace fa {
 
@@ -72,6 +73,66 @@ hipError_t launch_prefill_pp(FwdParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Compute units of the current device (cached per device).
+inline hipError_t device_cus(int* n) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < 64) {
+    const int c = cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *n = c;
+      return hipSuccess;
+    }
+  }
+  e = hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess && dev >= 0 && dev < 64) cus[dev].store(*n, std::memory_order_relaxed);
+  return e;
+}
+
+// Persistent ping-pong prefill (fa_prefill_persist.h) when the launch is a
+// large dense one it covers: equal query and key lengths with full 256-row
+// blocks (causal: an even number of them, paired), no window or offset, the
+// (batch, head) groups a multiple of the 8 XCDs, and a work list that splits
+// evenly over at least 3/4 of the CUs with at least two row blocks per
+// workgroup.  *launched is false (and nothing is launched) otherwise.
+template <class T, int D>
+hipError_t launch_prefill_persist(FwdParams p, hipStream_t st, bool* launched) {
+  using Tile = PingPongTile<D>;
+  *launched = false;
+  const bool causal = p.causal != 0;
+  const int64_t S = p.seqlen_q;
+  const int64_t G = (int64_t)p.batch * p.heads_q;
+  if (D != 128 || p.cu_q != nullptr || p.block_table != nullptr || S != p.seqlen_k ||
+      p.q_offset != 0 || p.window_left >= 0 || p.window_right >= 0 || S <= 0 ||
+      S % (causal ? 2 * Tile::BM : Tile::BM) != 0 || G % 8 != 0 || G > (1 << 24))
+    return hipSuccess;
+  int cus = 0;
+  hipError_t e = device_cus(&cus);
+  if (e != hipSuccess) return e;
+  const int64_t n_mb = S / Tile::BM;
+  const int64_t units = G / 8 * (causal ? n_mb / 2 : n_mb);   // per XCD
+  const int64_t max_slots = cus / 8;
+  int64_t slots = 0;
+  for (int64_t d = max_slots; d >= 1; --d)
+    if (units % d == 0) {
+      slots = d;
+      break;
+    }
+  const int64_t rounds = units / slots * (causal ? 2 : 1);
+  if (slots * 4 < max_slots * 3 || rounds < 2 || n_mb > (1 << 20)) return hipSuccess;
+  p.n_mblocks = (int)n_mb;
+  p.persist_rounds = (int)rounds;
+  auto kern = causal ? prefill_persist_kernel<T, D, true> : prefill_persist_kernel<T, D, false>;
+  static std::atomic<uint64_t> lds_devices_c{0}, lds_devices_n{0};
+  e = set_lds_limit(causal ? lds_devices_c : lds_devices_n, kern, Tile::LDS_BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(8 * slots)), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  *launched = true;
+  return hipGetLastError();
+}
+
 template <class T, int D, bool GEN>
 hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
   if constexpr (GEN) {
@@ -90,8 +151,11 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
     // of the block's window for all rows, and the softmax phase outgrows the
     // GEMM phase).
     if constexpr (!GEN) {
-      return p.cu_q != nullptr ? launch_prefill_pp<T, D, true>(p, st)
-                               : launch_prefill_pp<T, D, false>(p, st);
+      if (p.cu_q != nullptr) return launch_prefill_pp<T, D, true>(p, st);
+      bool launched = false;
+      hipError_t e = launch_prefill_persist<T, D>(p, st, &launched);
+      if (e != hipSuccess || launched) return e;
+      return launch_prefill_pp<T, D, false>(p, st);
     }
     // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
     // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves.
