@@ -14,6 +14,7 @@ as the reference's sequential checks would have.
 from __future__ import annotations
 
 import struct
+from contextlib import nullcontext as _nullcontext
 from typing import List, Optional
 
 import torch
@@ -30,13 +31,31 @@ def _decode(words: List[int], dtype: torch.dtype):
     return struct.unpack("<f" if dtype == torch.float32 else "<d", raw)[0]
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> "torch.cuda.Stream":
+    """A second stream per device (default priority) for argument checks."""
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    st = _SIDE_STREAMS.get(key)
+    if st is None:
+        st = torch.cuda.Stream(device=key)
+        _SIDE_STREAMS[key] = st
+    return st
+
+
 class Deferred:
-    def __init__(self) -> None:
+    def __init__(self, side: bool = False) -> None:
         # (kind, exception or None, lo, hi, device scalars); kind "flag": one
         # boolean, raise if true; "range": (min, max), raise if outside
         # [lo, hi]; "value": one scalar to return.
+        #
+        # side=True: range checks are reduced at flush time on a second
+        # stream that first waits for the current one, so a launch passed to
+        # flush() starts on the current stream without queueing behind them.
         self._items: list = []
         self._minmax: dict = {}   # id(tensor) -> (tensor, min, max): one aminmax per tensor
+        self._side = side
 
     def check(self, bad: torch.Tensor, exc: BaseException) -> None:
         """Queue ``raise exc`` if the device boolean ``bad`` is true."""
@@ -47,6 +66,9 @@ class Deferred:
         """Queue ``raise exc`` unless every element of the integer tensor ``t``
         lies in ``[lo, hi]`` (``None``: unbounded on that side)."""
         if t.numel() == 0:
+            return
+        if self._side:
+            self._items.append(("range", exc, lo, hi, [t]))
             return
         hit = self._minmax.get(id(t))
         if hit is None or hit[0] is not t:
@@ -71,32 +93,49 @@ class Deferred:
         stream), the queued scalars are copied to pinned host memory first,
         ``launch()`` runs, and only then does the host wait, for the copy
         alone: the launched work runs while the host reads the checks, and
-        a failing check still raises before this call returns.  Only kernels
-        that stay inside their buffers whatever the checked arrays hold may be
-        launched this way."""
+        a failing check still raises before this call returns.  With
+        ``side=True`` the reductions and the copy run on a second stream, so
+        the launch does not queue behind them.  Only kernels that stay inside
+        their buffers whatever the checked arrays hold may be launched this
+        way."""
         items, self._items = self._items, []
         self._minmax = {}
         if not items:
             if launch is not None:
                 launch()
             return []
-        scalars, dtypes = [], []
-        for it in items:
-            for s in it[4]:
-                s = s.reshape(1)
-                if s.dtype not in _WORDS:
-                    s = s.to(torch.int32 if s.dtype == torch.bool else torch.int64)
-                scalars.append(s.view(torch.int32))
-                dtypes.append(s.dtype)
-        packed = torch.cat(scalars) if len(scalars) > 1 else scalars[0]
-        if launch is None:
+        side = None
+        if self._side:
+            device = items[0][4][0].device
+            side = _side_stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):
+                reduced = []
+                for kind, exc, lo, hi, ts in items:
+                    if kind == "range":
+                        ts = [x.reshape(()) for x in torch.aminmax(ts[0])]
+                    reduced.append((kind, exc, lo, hi, ts))
+                items = reduced
+        with torch.cuda.stream(side) if side is not None else _nullcontext():
+            scalars, dtypes = [], []
+            for it in items:
+                for s in it[4]:
+                    s = s.reshape(1)
+                    if s.dtype not in _WORDS:
+                        s = s.to(torch.int32 if s.dtype == torch.bool else torch.int64)
+                    scalars.append(s.view(torch.int32))
+                    dtypes.append(s.dtype)
+            packed = torch.cat(scalars) if len(scalars) > 1 else scalars[0]
+            if launch is not None or side is not None:
+                host = torch.empty(packed.shape, dtype=packed.dtype, pin_memory=True)
+                host.copy_(packed, non_blocking=True)
+                done = torch.cuda.Event()
+                done.record()
+        if launch is None and side is None:
             words = packed.tolist()
         else:
-            host = torch.empty(packed.shape, dtype=packed.dtype, pin_memory=True)
-            host.copy_(packed, non_blocking=True)
-            done = torch.cuda.Event()
-            done.record()
-            launch()
+            if launch is not None:
+                launch()
             done.synchronize()
             words = host.tolist()
         host, pos = [], 0

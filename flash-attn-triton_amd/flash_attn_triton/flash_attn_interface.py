@@ -341,7 +341,14 @@ def flash_attn_with_kvcache(
     Returns (batch, seqlen_q, nheads, headdim).
     """
     paged = block_table is not None
-    chk = Deferred()
+    # Without an append, rotary or ALiBi slopes nothing the launch needs comes
+    # from the device checks, and the kernels keep every read inside the
+    # caches and the block table whatever cache_seqlens and block_table hold
+    # (fa_fwd_kvcache clamps them): the checks then run on a second stream
+    # and the attention launch goes out before the host waits for them; they
+    # still raise before this call returns.
+    launch_first = k is None and v is None and rotary_cos is None and alibi_slopes is None
+    chk = Deferred(side=launch_first)
     if (rotary_cos is None) != (rotary_sin is None):
         raise ValueError("rotary_cos and rotary_sin must be supplied together")
     if q.ndim != 4 or k_cache.ndim != 4 or v_cache.ndim != 4:
@@ -451,12 +458,6 @@ def flash_attn_with_kvcache(
         alibi = _normalize_alibi(alibi_slopes, q.shape[0], q.shape[2], q.device)
     except ValueError as exc:
         chk.fail(exc)
-    # Without an append, rotary or ALiBi slopes nothing the launch needs comes
-    # from the device checks, and the kernels keep every read inside the
-    # caches and the block table whatever cache_seqlens and block_table hold
-    # (fa_fwd_kvcache clamps them): the attention launch goes out before the
-    # host waits for the checks, which still raise before this call returns.
-    launch_first = n_new == 0 and cos_t is None and alibi is None
     if not launch_first:
         alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
         values = chk.flush()   # the one host synchronization of this call
