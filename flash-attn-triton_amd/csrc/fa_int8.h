@@ -8,11 +8,15 @@
 namespace fa {
 
 // x >= 0 ? floor(x + 0.5) : ceil(x - 0.5) in fp32 (the reference's _round_i8,
-// attention_kernel_int8.py:27-39).  No contraction: the two roundings of
-// x + 0.5 are part of the definition.
+// attention_kernel_int8.py:27-39), computed as trunc(x + copysign(0.5, x)):
+// the sum is the same single fp32 addition in both branches (x + 0.5 for
+// x >= 0, including +0 and -0, whose sum -0.5 truncates to 0 as floor(0.5)
+// does; x - 0.5 for x < 0), and truncation equals floor for the positive sums
+// and ceil for the negative ones.  No contraction: the rounding of the sum is
+// part of the definition.
 __device__ inline float round_half_away(float x) {
 #pragma clang fp contract(off)
-  return x >= 0.f ? floorf(x + 0.5f) : ceilf(x - 0.5f);
+  return __builtin_truncf(x + __builtin_copysignf(0.5f, x));
 }
 
 __device__ inline uint32_t pack_i8x4(float a, float b, float c, float d) {

@@ -62,6 +62,96 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
   if (sub == 0) s_k[row] = scale;
 }
 
+// Max over the LPR lanes of a row group (LPR = 4, 8, 16 or 32 consecutive
+// lanes) with DPP lane moves within 16-lane rows: quad swaps (xor 1, xor 2),
+// then the half-row and row mirrors; 32-lane groups add one exchange across
+// rows.
+template <int LPR>
+__device__ inline float group_max(float v) {
+  auto dpp = [](float x, auto ctrl) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), decltype(ctrl)::value,
+                                                      0xf, 0xf, false));
+  };
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0xB1>{}));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp(v, std::integral_constant<int, 0x4E>{}));   // quad_perm [2,3,0,1]
+  if constexpr (LPR >= 8) v = fmaxf(v, dpp(v, std::integral_constant<int, 0x141>{}));   // row_half_mirror
+  if constexpr (LPR >= 16) v = fmaxf(v, dpp(v, std::integral_constant<int, 0x140>{}));  // row_mirror
+  if constexpr (LPR >= 32) v = fmaxf(v, __shfl_xor(v, 16, 32));
+  return v;
+}
+
+// round_half_away(x) as an integer: the truncating convert of x +- 0.5 (the
+// same single fp32 addition, then the truncation the convert performs).
+__device__ inline int round_half_away_i(float x) {
+#pragma clang fp contract(off)
+  return (int)(x + __builtin_copysignf(0.5f, x));
+}
+
+// Low bytes of four ints in [-128, 127] as one dword (a in byte 0): two byte
+// permutes and a shift-or.
+__device__ inline uint32_t pack_i8x4_i(int a, int b, int c, int d) {
+  const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+  return ab | (cd << 16);
+}
+
+// The prepass for sequence lengths that are a multiple of 64 (every INT8
+// launch of the Python API): a workgroup quantizes 64 consecutive rows of one
+// (batch, head), whose addressing it computes once in scalar registers.  Four
+// lanes share a row, so the per-row work (the max across lanes, the two
+// divisions) is spread over D/4 values per lane; lane `sub` owns the 8-value
+// chunks sub, sub + 4, ..., so each load instruction reads 64 contiguous bytes
+// of a row and each store writes 32.  Every load is issued before any value
+// is converted.  Same arithmetic as quant_k_kernel.
+template <int D>
+__global__ __launch_bounds__(256) void quant_k64_kernel(const uint16_t* __restrict__ k,
+                                                        int8_t* __restrict__ k8,
+                                                        float* __restrict__ s_k, int heads,
+                                                        int seqlen, int64_t k_sb, int64_t k_sh,
+                                                        int64_t k_ss) {
+#pragma clang fp contract(off)
+  constexpr int NC = D / 32;             // 8-value chunks per lane
+  const int blocks_per_bh = seqlen >> 6;
+  const int bh = blockIdx.x / blocks_per_bh;
+  const int s0 = (blockIdx.x - bh * blocks_per_bh) << 6;
+  const int h = bh % heads;
+  const int b = bh / heads;
+  const int t = threadIdx.x;
+  const int sub = t & 3;
+  const int r = t >> 2;
+  const uint16_t* src =
+      k + (int64_t)b * k_sb + (int64_t)h * k_sh + (int64_t)(s0 + r) * k_ss + sub * 8;
+  u32x4 raw[NC];
+#pragma unroll
+  for (int i = 0; i < NC; ++i) raw[i] = load16(src + i * 32);
+  float x[NC][8];
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[i][e] = F16::to_float((uint16_t)(raw[i][e >> 1] >> ((e & 1) * 16)));
+      amax = fmaxf(amax, fabsf(x[i][e]));
+    }
+  }
+  amax = group_max<4>(amax);
+  const float scale = fmaxf(amax, 1.0f) / 127.0f;
+  const float inv = 1.0f / scale;
+  const int64_t row = (int64_t)bh * seqlen + s0 + r;
+  int8_t* dst = k8 + row * D + sub * 8;
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    int q[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) q[e] = round_half_away_i(x[i][e] * inv);
+    u32x2 out;
+    out[0] = pack_i8x4_i(q[0], q[1], q[2], q[3]);
+    out[1] = pack_i8x4_i(q[4], q[5], q[6], q[7]);
+    *reinterpret_cast<u32x2*>(dst + i * 32) = out;
+  }
+  if (sub == 0) s_k[row] = scale;
+}
+
 template <int D, int NW, int BN>
 struct Int8Tile {
   static constexpr int BM = NW * 32;
@@ -358,6 +448,13 @@ template <int D>
 hipError_t launch_quant_k(const void* k, int8_t* k8, float* s_k, int batch, int heads, int seqlen,
                           const int64_t* ks, hipStream_t st) {
   const int64_t rows = (int64_t)batch * heads * seqlen;
+  if (seqlen % 64 == 0 && rows / 64 <= 0x7fffffff) {
+    if (rows == 0) return hipSuccess;
+    hipLaunchKernelGGL(quant_k64_kernel<D>, dim3((unsigned)(rows / 64)), dim3(256), 0, st,
+                       static_cast<const uint16_t*>(k), k8, s_k, heads, seqlen, ks[0], ks[1],
+                       ks[2]);
+    return hipGetLastError();
+  }
   const int64_t threads = rows * (D / 8);
   const int64_t blocks = (threads + 255) / 256;
   if (blocks <= 0) return hipSuccess;

@@ -33,9 +33,26 @@ def test_quant_k_byte_exact(head_dim):
     # add rows that hit the clamp, exact zeros and x.5 ties
     k[0, 0, 0] = 0
     k[0, 0, 1] = torch.linspace(-0.9, 0.9, head_dim).half()
+    # amax 127 gives s = 1 exactly: every j + 0.5 is a tie, rounded away from
+    # zero; signed zeros quantize to 0.
+    ties = torch.arange(head_dim, dtype=torch.float32) - head_dim / 2 + 0.5
+    ties[0], ties[1], ties[2] = 127.0, -0.0, 0.0
+    k[1, 2, 5] = ties.half()
     k8, s_k = quantize_k_int8(k.to(DEV))
     torch.cuda.synchronize()
     ref8, refs = quant.quantize_k_rows(k.numpy().reshape(-1, 320, head_dim))
+    assert np.array_equal(k8.cpu().numpy(), ref8)
+    assert np.array_equal(s_k.cpu().numpy().view(np.uint32), refs.view(np.uint32))
+
+
+@pytest.mark.parametrize("seqlen", [100, 63, 1])
+def test_quant_k_lengths_not_multiple_of_64(seqlen):
+    # The row-per-thread prepass (lengths that are not a multiple of 64).
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import quantize_k_int8
+    k = _outlier_k(2, 3, seqlen, 128, 11)
+    k8, s_k = quantize_k_int8(k.to(DEV))
+    torch.cuda.synchronize()
+    ref8, refs = quant.quantize_k_rows(k.numpy().reshape(-1, seqlen, 128))
     assert np.array_equal(k8.cpu().numpy(), ref8)
     assert np.array_equal(s_k.cpu().numpy().view(np.uint32), refs.view(np.uint32))
 

