@@ -362,17 +362,20 @@ void prefill_persist_kernel(const FwdParams p) {
 
   // Softmax phase of the current block's tile j: the tile loads of K_{j+3}
   // and V_{j+2} (the next block's first tiles past the end), the softmax,
-  // then a wait for the previous phase's loads.
+  // then a wait for the loads of step j-2 (K_{j+1}, V_j), which the next
+  // GEMM phase reads; the loads of steps j-1 and j (and the Q prefetch of
+  // either) stay in flight.
   auto softmax_step = [&](int j) __attribute__((always_inline)) {
     load_tile(j + NS - 1, (j + NS - 1) % NS, true);
     load_tile(j + NS - 2, (j + NS - 2) % NS, false);
-    const bool pre = j == c_J - 4 && r_cur + 1 < rounds;
+    const bool more = r_cur + 1 < rounds;
+    const bool pre = j == c_J - 4 && more;
     if (pre) prefetch_q();
     softmax_tile(j);
-    if (pre)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * IPW + 1));
+    if ((pre || (j > 0 && j == c_J - 3)) && more)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * IPW + 1));
     else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * IPW));
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * IPW));
   };
 
   // ------------------------------------------------------------ prologue
