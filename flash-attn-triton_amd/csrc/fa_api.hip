@@ -185,7 +185,8 @@ int bwd_launch(const char* name, fa::BwdParams& p, int dtype, int64_t head_dim,
   p.causal = causal != 0;
   p.window_left = clamp_window(window_left);
   p.window_right = clamp_window(window_right);
-  const bool generic = alibi_slopes != nullptr || softcap > 0.f || p.drop.enabled;
+  const bool generic = alibi_slopes != nullptr || softcap > 0.f || p.drop.enabled ||
+                       p.bias != nullptr || p.dbias != nullptr;
   const hipError_t e = dtype == FA_DTYPE_F16 ? fa_launch_bwd_f16(p, (int)head_dim, generic, st)
                                              : fa_launch_bwd_bf16(p, (int)head_dim, generic, st);
   return hip_status(e, name);
@@ -357,8 +358,9 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
                  const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
-                 const float* alibi_slopes, int64_t alibi_batch_stride, float dropout_p,
-                 uint64_t dropout_seed, fa_stream_t stream) {
+                 const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
+                 const int64_t* bias_stride, float* dbias, const int64_t* dbias_stride,
+                 float dropout_p, uint64_t dropout_seed, fa_stream_t stream) {
   const char* name = "fa_bwd_dense";
   int rc = bwd_check_common(name, q, k, v, out, dout, lse, dq, dk, dv, delta, dtype, head_dim,
                             heads_q, heads_k);
@@ -366,6 +368,8 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
   if (!q_stride || !k_stride || !v_stride || !o_stride || !do_stride || !dq_stride ||
       !dk_stride || !dv_stride || !lse_stride)
     return fail(FA_ERR_INVALID, "%s: null stride argument", name);
+  if ((attn_bias && !bias_stride) || (dbias && !dbias_stride))
+    return fail(FA_ERR_INVALID, "%s: attn_bias / dbias without its strides", name);
   if (batch < 0 || seqlen_q < 0 || seqlen_k < 0)
     return fail(FA_ERR_INVALID, "%s: bad sizes B=%lld Sq=%lld Sk=%lld", name, (long long)batch,
                 (long long)seqlen_q, (long long)seqlen_k);
@@ -393,6 +397,16 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
   p.batch = (int)batch; p.seqlen_q = (int)seqlen_q; p.seqlen_k = (int)seqlen_k;
   p.heads_q = (int)heads_q; p.heads_k = (int)heads_k; p.group = (int)(heads_q / heads_k);
   p.q_offset = q_pos_offset;
+  p.bias = attn_bias;
+  if (attn_bias) {
+    p.bias_sb = bias_stride[0]; p.bias_sh = bias_stride[1];
+    p.bias_sq = bias_stride[2]; p.bias_sk = bias_stride[3];
+  }
+  p.dbias = dbias;
+  if (dbias) {
+    p.dbias_sb = dbias_stride[0]; p.dbias_sh = dbias_stride[1];
+    p.dbias_sq = dbias_stride[2]; p.dbias_sk = dbias_stride[3];
+  }
   return bwd_launch(name, p, dtype, head_dim, softmax_scale, softcap, alibi_slopes,
                     alibi_batch_stride, causal, window_left, window_right, dropout_p,
                     dropout_seed, (hipStream_t)stream);

@@ -34,6 +34,13 @@ struct BwdParams {
   int64_t q_offset;                               // query row i sits at position i + q_offset
   const int* cu_q; const int* cu_k;
   DropoutCfg drop;                                // the forward's dropout (GENERIC only)
+  // Optional fp32 additive bias of the dense forward (after ALiBi, before
+  // softcap), bias[b*bias_sb + h*bias_sh + i*bias_sq + j*bias_sk], and the
+  // fp32 buffer that receives its gradient dS, added at the same index form
+  // (dense layout only, GENERIC only; broadcast dims have stride 0, so their
+  // gradients sum).
+  const float* bias; int64_t bias_sb, bias_sh, bias_sq, bias_sk;
+  float* dbias; int64_t dbias_sb, dbias_sh, dbias_sq, dbias_sk;
   int n_blocks, total_blocks;                     // filled by the launcher
 };
 

@@ -82,14 +82,16 @@ __device__ inline u32x4 tr_operand(const uint16_t* tile, int lane, int cc, int c
 // Per-score transform shared by both kernels: the recomputed probability and
 // the softcap derivative.  `lse2` is the row's LSE in log2 units (the dQ
 // kernel passes +inf for a row that sees no key, giving P = 0; the dK/dV
-// kernel passes the row's -inf and masks every pair of such a row).
-template <bool GENERIC>
+// kernel passes the row's -inf and masks every pair of such a row); `bias_v`
+// is the pair's attn_bias value (read only by the BIAS instantiations).
+template <bool GENERIC, bool BIAS = false>
 __device__ inline float bwd_prob(const BwdParams& p, float s, float lse2, float slope, int qpos,
-                                 int key, float& cap_grad) {
+                                 int key, float bias_v, float& cap_grad) {
   cap_grad = 1.f;
   if (!GENERIC) return __builtin_amdgcn_exp2f(fmaf(s, p.scale_log2, -lse2));
   float x = s * p.scale;
   if (p.alibi != nullptr) x = fmaf(-slope, fabsf((float)(qpos - key)), x);
+  if (BIAS) x += bias_v;
   if (p.softcap > 0.f) {
     // tanh(x / softcap) = 1 - 2 / (1 + e^(2x/softcap))
     const float e2 = __builtin_amdgcn_exp2f(x * p.softcap_k);
@@ -140,10 +142,14 @@ struct BwdDqTile {
 };
 
 // VARLEN: cu_seqlens launch (an instantiation of its own, so that the dense
-// kernel carries none of the varlen work-item code).
-template <class T, int D, int NW, int BN, int NS, bool GENERIC, int WPE, bool VARLEN>
+// kernel carries none of the varlen work-item code).  BIAS: the dense
+// attn_bias and its gradient (instantiations of their own, so that the other
+// generic kernels keep their registers).
+template <class T, int D, int NW, int BN, int NS, bool GENERIC, int WPE, bool VARLEN,
+          bool BIAS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void bwd_dq_kernel(const BwdParams p) {
+  static_assert(!BIAS || (GENERIC && !VARLEN), "attn_bias: generic dense kernels only");
   using Tile = BwdDqTile<T, D, NW, BN, NS>;
   constexpr int BM = Tile::BM, TILEB = Tile::TILEB, IPW = Tile::IPW;
   constexpr int NKC = D / 16, NDB = D / 32, NKB = BN / 32, NCC = BN / 16;
@@ -234,6 +240,16 @@ void bwd_dq_kernel(const BwdParams p) {
     }
   }
   const float delta = halves_sum(dsum);
+  // attn_bias of this lane's row, and its gradient row (dense layout only).
+  const float* bias_row = nullptr;
+  float* dbias_row = nullptr;
+  if (BIAS && row_valid) {
+    if (p.bias != nullptr)
+      bias_row = p.bias + (int64_t)b * p.bias_sb + (int64_t)hh * p.bias_sh + (int64_t)qi * p.bias_sq;
+    if (p.dbias != nullptr)
+      dbias_row = p.dbias + (int64_t)b * p.dbias_sb + (int64_t)hh * p.dbias_sh +
+                  (int64_t)qi * p.dbias_sq;
+  }
   float lse2 = INFINITY;
   if (row_valid) {
     const float l = p.lse[lse_base + (int64_t)qi * p.lse_ss];
@@ -353,10 +369,16 @@ void bwd_dq_kernel(const BwdParams p) {
             const int v = o8 + 2 * j + u;
             const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
             float cg;
-            float pr = bwd_prob<GENERIC>(p, s[kb][v], lse2, slope, qpos, key, cg);
+            const float bv =
+                BIAS && bias_row != nullptr && key < Sk ? bias_row[(int64_t)key * p.bias_sk] : 0.f;
+            float pr = bwd_prob<GENERIC, BIAS>(p, s[kb][v], lse2, slope, qpos, key, bv, cg);
             if (MASKED) pr = (key < key_lo || key > key_hi) ? 0.f : pr;
             const float dpv = drop ? dp[kb][v] * dropout_factor(p.drop, rnd, 2 * j + u) : dp[kb][v];
             ds[u] = pr * (dpv - delta) * cg;
+            // dS is the gradient of the biased score; broadcast dims of the
+            // bias share an element, so the sum is accumulated atomically.
+            if (BIAS && dbias_row != nullptr && key < Sk && ds[u] != 0.f)
+              atomicAdd(dbias_row + (int64_t)key * p.dbias_sk, ds[u]);
           }
           dsb[cc][j] = T::pack2(ds[0], ds[1]);
         }
@@ -447,9 +469,11 @@ struct BwdDkvTile {
 // PASS 0 accumulates dK and dV together; at D = 256 the two accumulators do
 // not fit beside K and V, so the launcher runs PASS 1 (dV only) and PASS 2 (dK
 // only), recomputing S in each.
-template <class T, int D, int NW, int BM, int NS, bool GENERIC, int WPE, int PASS, bool VARLEN>
+template <class T, int D, int NW, int BM, int NS, bool GENERIC, int WPE, int PASS, bool VARLEN,
+          bool BIAS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void bwd_dkdv_kernel(const BwdParams p) {
+  static_assert(!BIAS || (GENERIC && !VARLEN), "attn_bias: generic dense kernels only");
   constexpr bool DO_DV = PASS != 2, DO_DK = PASS != 1;
   using Tile = BwdDkvTile<T, D, NW, BM, NS>;
   constexpr int BN = Tile::BN, TILEB = Tile::TILEB, IPW = Tile::IPW, LPS = Tile::LPS;
@@ -517,6 +541,12 @@ void bwd_dkdv_kernel(const BwdParams p) {
     // the first use of kreg.
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   }
+
+  // attn_bias column of this lane's key (dense layout only); the row and
+  // query head are added per score.
+  const float* bias_col = nullptr;
+  if (BIAS && key_valid && p.bias != nullptr)
+    bias_col = p.bias + (int64_t)b * p.bias_sb + (int64_t)kj * p.bias_sk;
 
   // Query rows i that see a key of this block: [q_lo, q_hi).
   int q_lo = 0, q_hi = Sq;
@@ -713,7 +743,10 @@ void bwd_dkdv_kernel(const BwdParams p) {
             const int row = m0 + r0 + (rr & 3) + (rr >= 4 ? 8 : 0);
             const int qpos = row + qoff;
             float cg;
-            float pr = bwd_prob<GENERIC>(p, s[rb][v], lse2, slope, qpos, kj, cg);
+            const float bv = BIAS && bias_col != nullptr && row < Sq
+                                 ? bias_col[(int64_t)hq * p.bias_sh + (int64_t)row * p.bias_sq]
+                                 : 0.f;
+            float pr = bwd_prob<GENERIC, BIAS>(p, s[rb][v], lse2, slope, qpos, kj, bv, cg);
             if (MASKED) {
               bool vis = true;
               if (causal) vis = vis && kj <= qpos;

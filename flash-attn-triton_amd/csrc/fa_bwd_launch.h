@@ -17,11 +17,12 @@ template <int D> struct BwdCfg {
   static constexpr int KV_NW = 4, KV_BM = D >= 128 ? 32 : 64, KV_NS = 3, KV_WPE = 1;
 };
 
-template <class T, int D, bool GEN, int PASS, bool VARLEN>
+template <class T, int D, bool GEN, int PASS, bool VARLEN, bool BIAS>
 hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
   using Tile = BwdDkvTile<T, D, C::KV_NW, C::KV_BM, C::KV_NS>;
-  auto kern = bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, C::KV_NS, GEN, C::KV_WPE, PASS, VARLEN>;
+  auto kern =
+      bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, C::KV_NS, GEN, C::KV_WPE, PASS, VARLEN, BIAS>;
   // The ALiBi slope table (one float per query head of the group) follows the
   // stages; the attribute allows the largest table that still fits.
   constexpr int kMaxLds = 160 * 1024;
@@ -39,12 +40,12 @@ hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <class T, int D, bool GEN, bool VARLEN>
+template <class T, int D, bool GEN, bool VARLEN, bool BIAS>
 hipError_t launch_bwd_v(BwdParams p, hipStream_t st) {
   using C = BwdCfg<D>;
   {
     using Tile = BwdDqTile<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS>;
-    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS, GEN, C::DQ_WPE, VARLEN>;
+    auto kern = bwd_dq_kernel<T, D, C::DQ_NW, C::DQ_BN, C::DQ_NS, GEN, C::DQ_WPE, VARLEN, BIAS>;
     static std::atomic<uint64_t> lds_devices{0};
     hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES);
     if (e != hipSuccess) return e;
@@ -59,18 +60,22 @@ hipError_t launch_bwd_v(BwdParams p, hipStream_t st) {
     }
   }
   if constexpr (D >= 256) {
-    hipError_t e = launch_dkdv<T, D, GEN, 1, VARLEN>(p, st);
+    hipError_t e = launch_dkdv<T, D, GEN, 1, VARLEN, BIAS>(p, st);
     if (e != hipSuccess) return e;
-    return launch_dkdv<T, D, GEN, 2, VARLEN>(p, st);
+    return launch_dkdv<T, D, GEN, 2, VARLEN, BIAS>(p, st);
   } else {
-    return launch_dkdv<T, D, GEN, 0, VARLEN>(p, st);
+    return launch_dkdv<T, D, GEN, 0, VARLEN, BIAS>(p, st);
   }
 }
 
+// attn_bias (dense only) selects the BIAS instantiations of the generic kernels.
 template <class T, int D, bool GEN>
 hipError_t launch_bwd_d(const BwdParams& p, hipStream_t st) {
-  return p.cu_q != nullptr ? launch_bwd_v<T, D, GEN, true>(p, st)
-                           : launch_bwd_v<T, D, GEN, false>(p, st);
+  if (p.cu_q != nullptr) return launch_bwd_v<T, D, GEN, true, false>(p, st);
+  if constexpr (GEN) {
+    if (p.bias != nullptr || p.dbias != nullptr) return launch_bwd_v<T, D, true, false, true>(p, st);
+  }
+  return launch_bwd_v<T, D, GEN, false, false>(p, st);
 }
 
 template <class T>

@@ -51,7 +51,8 @@ _SIGNATURES = {
                              _i64, _f32, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                              _f32, _u64, _vp]),
     "fa_bwd_dense": (_int, [_vp] * 10 + [_i64] * 6 + [_i64p] * 9 +
-                     [_int, _f32, _int, _i64, _i64, _i64, _f32, _vp, _i64, _f32, _u64, _vp]),
+                     [_int, _f32, _int, _i64, _i64, _i64, _f32, _vp, _i64, _vp, _i64p, _vp,
+                      _i64p, _f32, _u64, _vp]),
     "fa_bwd_varlen": (_int, [_vp] * 12 + [_i64] * 6 + [_i64p] * 9 +
                       [_int, _f32, _int, _i64, _i64, _f32, _vp, _i64, _f32, _u64, _vp]),
     "fa_fwd_kvcache_plan": (_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64, _i32p, _i64p]),
@@ -156,9 +157,12 @@ def fwd_dense(q, k, v, out, lse, softmax_scale: float, causal: bool, q_pos_offse
 
 def bwd_dense(q, k, v, out, dout, lse, dq, dk, dv, delta, softmax_scale: float, causal: bool,
               q_pos_offset: int, window_left: int, window_right: int, softcap: float,
-              alibi, dropout_p: float = 0.0, dropout_seed: int = 0) -> None:
+              alibi, dropout_p: float = 0.0, dropout_seed: int = 0, bias=None,
+              dbias=None) -> None:
     """Gradients of fwd_dense: all tensors BSHD ([B,S,H,D]); lse / delta fp32
-    [B,Hq,Sq]; dq/dk/dv are written.  See fa_bwd_dense."""
+    [B,Hq,Sq]; dq/dk/dv are written.  bias / dbias None or fp32 [B,Hq,Sq,Sk]
+    views (stride 0 on broadcast dims); dbias must hold zeros and receives the
+    bias gradient.  See fa_bwd_dense."""
     lib = load()
     B, Sq, Hq, D = q.shape
     Sk, Hk = k.shape[1], k.shape[2]
@@ -168,8 +172,10 @@ def bwd_dense(q, k, v, out, dout, lse, dq, dk, dv, delta, softmax_scale: float, 
         _ptr(dv), _ptr(delta), B, Sq, Sk, Hq, Hk, D, *st, _strides(lse.stride()),
         dtype_code(q.dtype), float(softmax_scale), int(bool(causal)), int(q_pos_offset),
         int(window_left), int(window_right), float(softcap), _ptr(alibi),
-        0 if alibi is None else int(alibi.stride(0)), float(dropout_p), int(dropout_seed),
-        _stream(q.device))
+        0 if alibi is None else int(alibi.stride(0)), _ptr(bias),
+        None if bias is None else _strides(bias.stride()), _ptr(dbias),
+        None if dbias is None else _strides(dbias.stride()), float(dropout_p),
+        int(dropout_seed), _stream(q.device))
     _check(status, "fa_bwd_dense")
 
 

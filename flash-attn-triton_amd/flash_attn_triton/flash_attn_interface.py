@@ -39,6 +39,7 @@ import torch
 
 from .triton_kernel.attention_kernel import (
     _kernel_ready,
+    _needs_grad,
     _wrap_grad,
     attention,
     attention_varlen,
@@ -67,8 +68,11 @@ def _normalize_alibi(alibi_slopes, batch, heads, device):
     return alibi_slopes.contiguous()
 
 
-def _bias_view(attn_bias, batch, heads, q_len, k_len, device):
-    """``attn_bias`` as an fp32 ``[B, H, Sq, Sk]`` view; broadcast dims get stride 0.
+def _bias4(attn_bias, batch, heads, q_len, k_len, device):
+    """``attn_bias`` as a 4-D fp32 tensor that broadcasts to the ``[B, H, Sq,
+    Sk]`` scores (leading size-1 dims added); the kernels read it through the
+    expanded view, whose broadcast dims have stride 0.  The conversion is a
+    differentiable torch op, so a gradient of this tensor reaches attn_bias.
 
     The reference adds it to the score tensor with torch broadcasting
     (flash_attn_interface.py:40-41), so any shape that broadcasts to the
@@ -78,12 +82,16 @@ def _bias_view(attn_bias, batch, heads, q_len, k_len, device):
     if bias.device != device:
         bias = bias.to(device)
     bias = bias.to(torch.float32)
+    shape = (batch, heads, q_len, k_len)
     try:
-        return torch.broadcast_to(bias, (batch, heads, q_len, k_len))
-    except RuntimeError as exc:
+        fits = bias.ndim <= 4 and torch.broadcast_shapes(tuple(bias.shape), shape) == shape
+    except RuntimeError:
+        fits = False
+    if not fits:
         raise ValueError(
             f"attn_bias of shape {tuple(bias.shape)} does not broadcast to the scores "
-            f"({batch}, {heads}, {q_len}, {k_len})") from exc
+            f"({batch}, {heads}, {q_len}, {k_len})")
+    return bias.reshape((1,) * (4 - bias.ndim) + tuple(bias.shape))
 
 
 def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
@@ -108,7 +116,7 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
     bias = None
     if attn_bias is not None:
-        bias = _bias_view(attn_bias, batch, q_heads, q_len, k_len, q.device)
+        bias = _bias4(attn_bias, batch, q_heads, q_len, k_len, q.device)
     alibi = None
     if alibi_slopes is not None:
         alibi = _normalize_alibi(alibi_slopes, batch, q_heads, q.device)
@@ -120,7 +128,9 @@ def _attention_with_probs(q, k, v, dropout_p, softmax_scale, causal, window_size
     probs = torch.empty((batch, q_heads, q_len, k_len), dtype=torch.float32, device=q.device)
     _native.attn_probs(_kernel_ready(q), _kernel_ready(k), lse, probs, None, None, None,
                        q_len, k_len, scale, causal, causal_offset, window_size[0],
-                       window_size[1], softcap, alibi, bias, dropout_p, seed)
+                       window_size[1], softcap, alibi,
+                       None if bias is None else bias.detach().expand(batch, q_heads, q_len, k_len),
+                       dropout_p, seed)
     return out, lse, probs
 
 
@@ -508,7 +518,8 @@ def _compact_varlen(q, k, v, cu_q, cu_k, used_q, used_k, block_table):
     sequence and the keys of a paged cache in order; the reference builds its
     inputs this way (flash_attn_interface.py:533-581).  Only the
     ``return_attn_probs`` path, which materialises probabilities anyway, uses
-    it: the kernels read seqused_* and the block table directly."""
+    it, and so do gradients through seqused_* and the block table: the forward
+    kernels read seqused_* and the block table directly."""
     dev = q.device
     cq, ck = cu_q.tolist(), cu_k.tolist()
     lq = [b - a for a, b in zip(cq[:-1], cq[1:])]
@@ -701,8 +712,19 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     if seqused_q is not None:
         cu_out = torch.zeros((batch_size + 1,), dtype=torch.int32, device=q.device)
         torch.cumsum(seqused_q, 0, out=cu_out[1:])
+    if (paged or seqused_q is not None or seqused_k is not None) and _needs_grad(q, k, v):
+        # Gradients: as the reference (:533-581), gather the used rows and the
+        # paged keys into packed tensors (indexing that autograd scatters back
+        # to q, k, v and the cache), then run the varlen forward and backward
+        # on them.
+        q, k, v, cu_seqlens_q, cu_seqlens_k = _compact_varlen(
+            q, k, v, cu_seqlens_q, cu_seqlens_k, seqused_q, seqused_k, block_table)
+        return varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                                softmax_scale=softmax_scale, causal=causal,
+                                window_left=window_size[0], window_right=window_size[1],
+                                softcap=softcap, alibi=alibi if use_alibi else None,
+                                dropout_p=dropout_p, dropout_seed=seed)
     if paged or seqused_q is not None or seqused_k is not None:
-        # Forward only: gradients through the block table and used counts are not built.
         out = varlen_forward(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                              softmax_scale=softmax_scale, causal=causal,
                              window_left=window_size[0], window_right=window_size[1],
@@ -711,7 +733,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                              out_rows=values[out_rows] if out_rows is not None else None,
                              cu_out=cu_out, block_table=block_table, dropout_p=dropout_p,
                              dropout_seed=seed)
-        return _wrap_grad(out, q, k, v)
+        return out
     return varlen_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                             softmax_scale=softmax_scale, causal=causal,
                             window_left=window_size[0], window_right=window_size[1],

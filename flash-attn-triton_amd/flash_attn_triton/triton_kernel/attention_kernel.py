@@ -10,13 +10,15 @@ Both call the gfx950 HIP kernels of ``libfa_gfx950.so`` through ``_native``.
 The kernels handle ragged lengths, strided inputs and grouped KV heads
 directly, so nothing is padded, repeated or copied on the host.
 
-Autograd: when q, k or v requires grad the forward also keeps the LSE and the
-backward runs ``fa_bwd_dense`` / ``fa_bwd_varlen`` (the reference's
-``_attention.backward`` :1185-1198 and ``_attention_varlen.backward``
-:1322-1361), fp16 and bf16.  Not differentiable (backward raises
-``NotImplementedError``): fp32 inputs, ``attn_bias``, seqused / paged varlen
-and the KV-cache path.  Dropout (``dropout_p > 0``) drops probabilities with
-the counter-based Philox mask of the kernels; the seed is drawn from torch's
+Autograd: when q, k or v (or the dense path's ``attn_bias``) requires grad
+the forward also keeps the LSE and the backward runs ``fa_bwd_dense`` /
+``fa_bwd_varlen`` (the reference's ``_attention.backward`` :1185-1198 and
+``_attention_varlen.backward`` :1322-1361), fp16 and bf16; the bias gradient
+is dS summed over the bias's broadcast dimensions, as torch autograd gives it
+for the reference's math path (flash_attn_interface.py:15-49).  Not
+differentiable (backward raises ``NotImplementedError``): fp32 inputs and the
+KV-cache path.  Dropout (``dropout_p > 0``) drops probabilities with the
+counter-based Philox mask of the kernels; the seed is drawn from torch's
 default CPU generator unless given, and the backward replays the same mask.
 """
 from __future__ import annotations
@@ -33,8 +35,8 @@ __all__ = ["attention", "attention_varlen", "dense_forward", "varlen_forward", "
            "FORWARD_ONLY_MSG"]
 
 FORWARD_ONLY_MSG = (
-    "flash_attn_triton (gfx950 HIP build): this call has no backward (fp32 inputs, "
-    "attn_bias, seqused / paged varlen and the KV-cache path are forward only)")
+    "flash_attn_triton (gfx950 HIP build): this call has no backward (fp32 inputs and "
+    "the KV-cache path are forward only)")
 
 
 def new_dropout_seed() -> int:
@@ -145,10 +147,14 @@ def _f32_alibi(alibi, device):
 def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: bool,
                    q_pos_offset: int = 0, window_left: int = -1, window_right: int = -1,
                    softcap: float = 0.0, alibi: Optional[torch.Tensor] = None,
-                   dropout_p: float = 0.0, dropout_seed: int = 0):
+                   dropout_p: float = 0.0, dropout_seed: int = 0,
+                   bias: Optional[torch.Tensor] = None, dbias: Optional[torch.Tensor] = None):
     """Gradients ``(dq, dk, dv)`` of ``dense_forward`` from ``dout``, given its
     output and LSE (``fa_bwd_dense``).  Head dim 16 runs at 32 with zero padding
-    (the extra dims contribute nothing to the scores and get zero gradients)."""
+    (the extra dims contribute nothing to the scores and get zero gradients).
+    ``bias``: the forward's fp32 ``[B, Hq, Sq, Sk]`` view; ``dbias`` (optional):
+    a zero-filled fp32 view of the same shape whose broadcast dims have stride
+    0, which receives the bias gradient."""
     if q.dtype == torch.float32:
         raise NotImplementedError(
             "flash_attn_triton (gfx950 HIP build): the backward takes fp16 or bf16 inputs; "
@@ -158,7 +164,8 @@ def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: boo
                                softmax_scale=softmax_scale, causal=causal,
                                q_pos_offset=q_pos_offset, window_left=window_left,
                                window_right=window_right, softcap=softcap, alibi=alibi,
-                               dropout_p=dropout_p, dropout_seed=dropout_seed)
+                               dropout_p=dropout_p, dropout_seed=dropout_seed, bias=bias,
+                               dbias=dbias)
         return tuple(g[..., :16] for g in grads)
     qk, kk, vk, ok, dok = (_kernel_ready(t) for t in (q, k, v, out, dout))
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -167,7 +174,8 @@ def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: boo
     delta = torch.empty_like(lse)
     _native.bwd_dense(qk, kk, vk, ok, dok, lse, dq, dk, dv, delta, softmax_scale, causal,
                       q_pos_offset, window_left, window_right, softcap,
-                      _f32_alibi(alibi, q.device), dropout_p, dropout_seed)
+                      _f32_alibi(alibi, q.device), dropout_p, dropout_seed, bias=bias,
+                      dbias=dbias)
     return dq, dk, dv
 
 
@@ -203,17 +211,29 @@ def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, max_seqlen_q: int, max_
     return dq, dk, dv
 
 
+def _expand_bias(bias4: torch.Tensor, q: torch.Tensor, k: torch.Tensor) -> torch.Tensor:
+    """A 4-D fp32 bias as the ``[B, Hq, Sq, Sk]`` score view (stride 0 on its
+    size-1 dims)."""
+    return bias4.expand(q.shape[0], q.shape[2], q.shape[1], k.shape[1])
+
+
 class _DenseAttention(torch.autograd.Function):
-    """dense_forward with the fa_bwd_dense backward; returns (out, lse)."""
+    """dense_forward with the fa_bwd_dense backward; returns (out, lse).
+
+    ``bias4`` (optional) is the attn_bias as a 4-D fp32 tensor that broadcasts
+    to the scores; its gradient comes back in that shape, summed over the
+    broadcast dimensions."""
 
     @staticmethod
     def forward(ctx, q, k, v, softmax_scale, causal, q_pos_offset, window_left, window_right,
-                softcap, alibi, dropout_p, dropout_seed):
+                softcap, alibi, dropout_p, dropout_seed, bias4):
+        bias = None if bias4 is None else _expand_bias(bias4, q, k)
         out, lse = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
                                  q_pos_offset=q_pos_offset, window_left=window_left,
                                  window_right=window_right, softcap=softcap, alibi=alibi,
-                                 return_lse=True, dropout_p=dropout_p, dropout_seed=dropout_seed)
-        ctx.save_for_backward(q, k, v, out, lse, alibi)
+                                 return_lse=True, bias=bias, dropout_p=dropout_p,
+                                 dropout_seed=dropout_seed)
+        ctx.save_for_backward(q, k, v, out, lse, alibi, bias4)
         ctx.opts = (softmax_scale, causal, q_pos_offset, window_left, window_right, softcap,
                     dropout_p, dropout_seed)
         ctx.mark_non_differentiable(lse)
@@ -221,12 +241,19 @@ class _DenseAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout, _dlse):
-        q, k, v, out, lse, alibi = ctx.saved_tensors
+        q, k, v, out, lse, alibi, bias4 = ctx.saved_tensors
         scale, causal, off, wl, wr, cap, dp, seed = ctx.opts
+        bias = dbias4 = dbias = None
+        if bias4 is not None:
+            bias = _expand_bias(bias4, q, k)
+            if ctx.needs_input_grad[12]:
+                dbias4 = torch.zeros(bias4.shape, dtype=torch.float32, device=q.device)
+                dbias = _expand_bias(dbias4, q, k)
         dq, dk, dv = dense_backward(q, k, v, out, dout, lse, softmax_scale=scale, causal=causal,
                                     q_pos_offset=off, window_left=wl, window_right=wr,
-                                    softcap=cap, alibi=alibi, dropout_p=dp, dropout_seed=seed)
-        return (dq, dk, dv) + (None,) * 9
+                                    softcap=cap, alibi=alibi, dropout_p=dp, dropout_seed=seed,
+                                    bias=bias, dbias=dbias)
+        return (dq, dk, dv) + (None,) * 9 + (dbias4,)
 
 
 class _VarlenAttention(torch.autograd.Function):
@@ -262,18 +289,19 @@ def dense_attention(q, k, v, *, softmax_scale: float, causal: bool, q_pos_offset
                     alibi: Optional[torch.Tensor] = None, return_lse: bool = False,
                     bias: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
                     dropout_seed: int = 0):
-    """``dense_forward`` that is differentiable in q, k, v (fp16 / bf16)."""
-    if not _needs_grad(q, k, v) or bias is not None:
+    """``dense_forward`` that is differentiable in q, k, v and ``bias`` (fp16 /
+    bf16).  ``bias`` (optional) is a 4-D fp32 tensor that broadcasts to the
+    ``[B, Hq, Sq, Sk]`` scores."""
+    if not _needs_grad(q, k, v, bias):
         res = dense_forward(q, k, v, softmax_scale=softmax_scale, causal=causal,
                             q_pos_offset=q_pos_offset, window_left=window_left,
                             window_right=window_right, softcap=softcap, alibi=alibi,
-                            return_lse=return_lse, bias=bias, dropout_p=dropout_p,
-                            dropout_seed=dropout_seed)
-        if return_lse:
-            return _wrap_grad(res[0], q, k, v), res[1]
-        return _wrap_grad(res, q, k, v)
+                            return_lse=return_lse,
+                            bias=None if bias is None else _expand_bias(bias, q, k),
+                            dropout_p=dropout_p, dropout_seed=dropout_seed)
+        return res
     out, lse = _DenseAttention.apply(q, k, v, softmax_scale, causal, q_pos_offset, window_left,
-                                     window_right, softcap, alibi, dropout_p, dropout_seed)
+                                     window_right, softcap, alibi, dropout_p, dropout_seed, bias)
     return (out, lse) if return_lse else out
 
 

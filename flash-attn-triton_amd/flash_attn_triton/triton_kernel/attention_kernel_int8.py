@@ -10,7 +10,12 @@ and PV in fp16.
 
 The reference gates this path to Turing (compute capability 7.5,
 :275-279); this build gates it to gfx950 (the only target it is compiled
-for).  Only the forward pass exists; backward raises ``NotImplementedError``.
+for).
+
+Backward: as the reference's ``_attention_int8.backward`` (:255-267), the
+gradients come from the dense fp16 backward (``fa_bwd_dense``) on the
+unquantized q, k, v with the INT8 forward's output and LSE; keys at or past
+``seq_len_k`` get zero gradients.
 """
 from __future__ import annotations
 
@@ -19,7 +24,7 @@ import math
 import torch
 
 from .. import _native
-from .attention_kernel import _wrap_grad
+from .attention_kernel import _needs_grad, dense_backward
 
 __all__ = ["attention_int8", "quantize_k_int8"]
 
@@ -65,7 +70,45 @@ def attention_int8(q, k, v, causal=False, sm_scale=None, seq_len_k=None, seq_len
         seq_len_k = q.shape[2]
     if seq_len_q is None:
         seq_len_q = q.shape[2]
+    if _needs_grad(q, k, v):
+        return _Int8Attention.apply(q, k, v, causal, sm_scale, seq_len_k, seq_len_q)
+    return _int8_forward(q, k, v, causal, sm_scale, seq_len_k, seq_len_q, None)
+
+
+def _int8_forward(q, k, v, causal, sm_scale, seq_len_k, seq_len_q, lse):
     k8, s_k = quantize_k_int8(k)
     out = torch.empty_like(q)
-    _native.fwd_int8(q, k8, s_k, v, out, None, sm_scale, causal, seq_len_k, seq_len_q)
-    return _wrap_grad(out, q, k, v)
+    _native.fwd_int8(q, k8, s_k, v, out, lse, sm_scale, causal, seq_len_k, seq_len_q)
+    return out
+
+
+class _Int8Attention(torch.autograd.Function):
+    """INT8 forward; fp16 dense backward (reference attention_kernel_int8.py:255-267)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, causal, sm_scale, seq_len_k, seq_len_q):
+        B, H, S, _ = q.shape
+        lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+        out = _int8_forward(q, k, v, causal, sm_scale, seq_len_k, seq_len_q, lse)
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.opts = (causal, sm_scale, seq_len_k, seq_len_q)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, out, lse = ctx.saved_tensors
+        causal, sm_scale, seq_len_k, seq_len_q = ctx.opts
+        lk = max(0, min(int(seq_len_k), k.shape[2]))
+        if lk == 0:   # no visible key: the output is zero and so are the gradients
+            return torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), None, None, None, None
+        # The INT8 kernel's query row i sits at position i + seq_len_k - seq_len_q
+        # and sees keys [0, seq_len_k): the dense layout over k[:, :, :seq_len_k].
+        dq, dk_used, dv_used = dense_backward(
+            q.transpose(1, 2), k.transpose(1, 2)[:, :lk], v.transpose(1, 2)[:, :lk],
+            out.transpose(1, 2), dout.transpose(1, 2), lse, softmax_scale=sm_scale,
+            causal=bool(causal), q_pos_offset=int(seq_len_k) - int(seq_len_q))
+        dk = torch.zeros_like(k)
+        dv = torch.zeros_like(v)
+        dk[:, :, :lk] = dk_used.transpose(1, 2)
+        dv[:, :, :lk] = dv_used.transpose(1, 2)
+        return dq.transpose(1, 2), dk, dv, None, None, None, None

@@ -136,11 +136,19 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
  * seq, head} (k, v, dk, dv with Hk heads); lse is the natural-log LSE the
  * forward returned ([B, Hq, Sq] at lse_stride {batch, head, seq}); delta is an
  * fp32 workspace of the same shape and strides (written, then read).  The
- * score options (scale, causal, q_pos_offset, window, softcap, ALiBi) must be
- * those of the forward call.  dq / dk / dv are written, not accumulated; grouped
- * KV heads are reduced inside the kernel (no atomics, deterministic).  dtype
- * fp16 or bf16; head_dim 32, 64, 128 or 256.  Launches two kernels on
- * `stream`.
+ * score options (scale, causal, q_pos_offset, window, softcap, ALiBi,
+ * attn_bias) must be those of the forward call.  dq / dk / dv are written, not
+ * accumulated; grouped KV heads are reduced inside the kernel (no atomics,
+ * deterministic).  dtype fp16 or bf16; head_dim 32, 64, 128 or 256.
+ *
+ * attn_bias / bias_stride[4]: the forward's fp32 bias (may be null).  dbias /
+ * dbias_stride[4] (may be null): an fp32 buffer, zero-filled by the caller,
+ * that receives d loss / d bias, i.e. dS = P (dP - delta) (times the softcap
+ * derivative) at dbias[b*s0 + h*s1 + i*s2 + j*s3]; give broadcast dimensions
+ * stride 0 and their gradients are summed (atomically: with a broadcast bias
+ * the summation order, and so the last bits, vary between calls).  The
+ * reference differentiates its torch path through the bias
+ * (flash_attn_interface.py:15-49).  Launches two kernels on `stream`.
  */
 int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, const void* dout,
                  const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t batch,
@@ -150,8 +158,9 @@ int fa_bwd_dense(const void* q, const void* k, const void* v, const void* out, c
                  const int64_t* dq_stride, const int64_t* dk_stride, const int64_t* dv_stride,
                  const int64_t* lse_stride, int dtype, float softmax_scale, int causal,
                  int64_t q_pos_offset, int64_t window_left, int64_t window_right, float softcap,
-                 const float* alibi_slopes, int64_t alibi_batch_stride, float dropout_p,
-                 uint64_t dropout_seed, fa_stream_t stream);
+                 const float* alibi_slopes, int64_t alibi_batch_stride, const float* attn_bias,
+                 const int64_t* bias_stride, float* dbias, const int64_t* dbias_stride,
+                 float dropout_p, uint64_t dropout_seed, fa_stream_t stream);
 
 /* Backward of fa_fwd_varlen (without seqused / block table).
  *

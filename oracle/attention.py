@@ -188,8 +188,8 @@ def attention(q, k, v, softmax_scale: Optional[float] = None, causal: bool = Fal
 def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
                        causal: bool = False, window_size: Sequence[int] = (-1, -1),
                        softcap: float = 0.0, alibi_slopes=None, causal_offset: int = 0,
-                       dropout_p: float = 0.0, dropout_seed: int = 0, batch_ids=None
-                       ) -> Tuple[np.ndarray, np.ndarray, np.ndarray]:
+                       dropout_p: float = 0.0, dropout_seed: int = 0, batch_ids=None,
+                       attn_bias=None, return_dbias: bool = False):
     """Exact gradients ``(dq, dk, dv)`` of :func:`attention`'s output against
     ``dout [B,Sq,Hq,D]``, in float64.
 
@@ -204,6 +204,12 @@ def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
     reference's kernels use ``F P (dP - delta)`` (attention_kernel.py:661,
     :763), which drops the ``- P delta`` term of dropped elements; this is
     the derivative of the forward above.
+
+    ``attn_bias`` (anything that broadcasts to ``[B,Hq,Sq,Sk]``) is added to
+    the scaled scores before softcap, as in :func:`attention`; with
+    ``return_dbias`` the result gains a fourth entry, ``dS`` summed to the
+    bias's own shape (what torch autograd gives the reference's math path,
+    flash_attn_interface.py:40-41).
     """
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
@@ -214,7 +220,7 @@ def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
     rep = q_heads // kv_heads
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else float(softmax_scale)
     out, _, probs = attention(q, k, v, scale, causal, window_size, softcap, alibi_slopes,
-                              None, causal_offset)
+                              attn_bias, causal_offset)
     fac = None
     if dropout_p > 0:
         ids = np.arange(batch) if batch_ids is None else batch_ids
@@ -241,11 +247,19 @@ def attention_backward(q, k, v, dout, softmax_scale: Optional[float] = None,
             q_pos = np.arange(q_len) + int(causal_offset)
             dist = np.abs(q_pos[:, None] - np.arange(k_len)[None, :]).astype(np.float64)
             raw = raw - slopes[:, :, None, None] * dist[None, None]
+        if attn_bias is not None:
+            raw = raw + np.asarray(attn_bias, dtype=np.float64)
         ds = ds * (1.0 - np.tanh(raw / softcap) ** 2)
     dq = (np.matmul(ds, kr) * scale).transpose(0, 2, 1, 3)
     dk_h = np.matmul(ds.transpose(0, 1, 3, 2), qh) * scale
     dk = dk_h.reshape(batch, kv_heads, rep, k_len, head_dim).sum(axis=2).transpose(0, 2, 1, 3)
     dv = dv_h.reshape(batch, kv_heads, rep, k_len, head_dim).sum(axis=2).transpose(0, 2, 1, 3)
+    if return_dbias:
+        shape = np.shape(attn_bias)
+        full = (1,) * (4 - len(shape)) + tuple(shape)
+        axes = tuple(i for i in range(4) if full[i] == 1 and ds.shape[i] != 1)
+        dbias = np.sum(ds, axis=axes, keepdims=True).reshape(shape)
+        return dq, dk, dv, dbias
     return dq, dk, dv
 
 

@@ -212,7 +212,66 @@ def test_forward_only_paths_raise_on_backward():
     out = flash_attn_func(q, q, q)
     with pytest.raises(NotImplementedError):
         out.sum().backward()
-    q16 = randn((1, 64, 2, 64), 101).to(DEV).requires_grad_()
-    out = flash_attn_func(q16, q16, q16, attn_bias=torch.zeros((64, 64), device=DEV))
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
+
+
+def _bias_case(bias_shape, B=2, Sq=150, Sk=190, Hq=4, Hk=2, D=64, dtype=torch.float16,
+               seed=0, causal=False, softcap=0.0, alibi=False, bias_dtype=torch.float32,
+               window=(-1, -1)):
+    """Gradients through attn_bias: the reference's math path is differentiated
+    by torch autograd, so d bias is dS summed over the bias's broadcast dims."""
+    from flash_attn_triton import flash_attn_func
+    q = randn((B, Sq, Hq, D), seed + 1, dtype)
+    k = randn((B, Sk, Hk, D), seed + 2, dtype)
+    v = randn((B, Sk, Hk, D), seed + 3, dtype)
+    do = randn((B, Sq, Hq, D), seed + 4, dtype)
+    bias = randn(bias_shape, seed + 5, torch.float32).to(bias_dtype)
+    slopes = (torch.rand(Hq, generator=torch.Generator().manual_seed(seed + 6)) * 0.3
+              if alibi else None)
+    qd, kd, vd, bd = (t.to(DEV).requires_grad_() for t in (q, k, v, bias))
+    out = flash_attn_func(qd, kd, vd, causal=causal, softcap=softcap, window_size=window,
+                          alibi_slopes=None if slopes is None else slopes.to(DEV), attn_bias=bd)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    ref = ora.attention_backward(to_np(q), to_np(k), to_np(v), to_np(do), None, causal, window,
+                                 softcap, None if slopes is None else slopes.double().numpy(),
+                                 attn_bias=bias.double().numpy(), return_dbias=True)
+    for name, t, r in zip(("dq", "dk", "dv"), (qd, kd, vd), ref):
+        _check(name, t.grad, r, dtype)
+    assert bd.grad.shape == bias.shape and bd.grad.dtype == bias_dtype
+    # d bias sums dS over the broadcast dims: the bar scales with the count.
+    summed = (B * Hq * Sq * Sk) // int(np.prod(bias_shape))
+    got = to_np(bd.grad.float().cpu())
+    err = np.abs(got - ref[3])
+    bound = GRAD_ATOL[dtype] * math.sqrt(summed) + GRAD_RTOL[dtype] * np.abs(ref[3])
+    print(f"dbias {tuple(bias_shape)}: max-abs err {float(np.max(err)):.3e} "
+          f"(max |exact| {float(np.max(np.abs(ref[3]))):.3e})")
+    assert np.all(np.isfinite(got)) and np.all(err <= bound), float(np.max(err - bound))
+
+
+@pytest.mark.parametrize("bias_shape", [(2, 4, 150, 150), (1, 1, 150, 150), (150, 150),
+                                        (2, 1, 1, 150), (4, 150, 1)])
+def test_attn_bias_gradients(bias_shape):
+    _bias_case(bias_shape, Sq=150, Sk=150, causal=True, seed=110)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attn_bias_gradients_with_features(dtype):
+    # Softcap (the bias sits inside the tanh), ALiBi and a window; fp16 bias;
+    # D = 128 and D = 32.
+    _bias_case((2, 4, 200, 200), Sq=200, Sk=200, D=128, dtype=dtype, causal=True, softcap=15.0,
+               alibi=True, window=(64, 0), seed=120, bias_dtype=torch.float16)
+    _bias_case((1, 4, 96, 96), Sq=96, Sk=96, D=32, dtype=dtype, causal=False, softcap=0.0,
+               seed=121)
+
+
+def test_attn_bias_gradients_only_bias():
+    # q, k, v without grad: the bias alone is differentiated.
+    from flash_attn_triton import flash_attn_func
+    q, k, v = (randn((1, 64, 2, 64), s).to(DEV) for s in (131, 132, 133))
+    bias = randn((1, 2, 64, 64), 134, torch.float32).to(DEV).requires_grad_()
+    do = randn((1, 64, 2, 64), 135)
+    flash_attn_func(q, k, v, attn_bias=bias).backward(do.to(DEV))
+    ref = ora.attention_backward(*(to_np(t.cpu()) for t in (q, k, v)), to_np(do), None, False,
+                                 attn_bias=to_np(bias.detach().cpu()), return_dbias=True)
+    np.testing.assert_allclose(to_np(bias.grad.cpu()), ref[3], atol=GRAD_ATOL[torch.float16],
+                               rtol=GRAD_RTOL[torch.float16])

@@ -148,3 +148,49 @@ def test_int8_baseline_c3_sampled(causal):
                                       causal=causal, q_positions=[i])
         assert_close(to_np(out[b, h, i]), ref[0, 0, 0], INT8_ATOL, f"b={b} h={h} i={i}",
                      torch.float16)
+
+
+def _int8_grad_check(name, got, exact):
+    # The reference's INT8 gradient bars against unquantized attention
+    # (tests/test_compare_implementations.py:27-28, :221-235): the INT8
+    # forward's output and LSE feed the fp16 dense backward.
+    got = to_np(got.cpu())
+    err = np.abs(got - exact)
+    bound = 5e-2 + 2e-2 * np.abs(exact)
+    print(f"int8 backward {name}: max-abs err {float(np.max(err)):.3e}")
+    assert np.all(np.isfinite(got)) and np.all(err <= bound), (
+        f"{name}: max |err| {float(np.max(err)):.3e}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_int8_gradients(causal):
+    # The reference's case: B2 H2 S128 D64, scale 0.125, two query and two
+    # key blocks per head.
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import attention_int8
+    q, k, v, do = (randn((2, 2, 128, 64), s) for s in (201, 202, 203, 204))
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = attention_int8(qd, kd, vd, causal=causal, sm_scale=0.125)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    ref = ora.attention_backward(*(to_np(t.transpose(1, 2)) for t in (q, k, v, do)), 0.125, causal)
+    for name, t, r in zip(("dq", "dk", "dv"), (qd, kd, vd), ref):
+        _int8_grad_check(name, t.grad.transpose(1, 2), r)
+
+
+def test_int8_gradients_with_short_key_length():
+    # seq_len_k = 100 of 128 keys visible, query row i at position
+    # i + seq_len_k - seq_len_q: keys 100.. get exactly zero gradients.
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import attention_int8
+    q, k, v, do = (randn((1, 2, 128, 64), s) for s in (211, 212, 213, 214))
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = attention_int8(qd, kd, vd, causal=True, seq_len_k=100, seq_len_q=128)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(kd.grad[:, :, 100:]) == 0
+    assert torch.count_nonzero(vd.grad[:, :, 100:]) == 0
+    ref = ora.attention_backward(*(to_np(t.transpose(1, 2)) for t in (q, k[:, :, :100], v[:, :, :100],
+                                                                         do)),
+                                 None, True, causal_offset=100 - 128)
+    for name, t, r in zip(("dq", "dk", "dv"), (qd.grad, kd.grad[:, :, :100], vd.grad[:, :, :100]),
+                          ref):
+        _int8_grad_check(name, t.transpose(1, 2), r)

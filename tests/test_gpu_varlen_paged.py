@@ -151,3 +151,74 @@ def test_errors_follow_the_reference():
                                                            device=DEV), 6, 9, block_table=bt_ok)
     with pytest.raises(ValueError, match=r"shape \(batch, max_num_pages\)"):
         flash_attn_varlen_func(q, kc, kc, cu, cu, 6, 6, block_table=bt_ok[:1])
+
+
+def _grad_case(lq, lk, *, hq=4, hk=2, d=64, dtype=torch.float16, seed=0, used_q=None,
+               used_k=None, page=None, causal=False, **kw):
+    """Gradients through seqused_* and the block table: the reference gathers
+    the used rows / pages with torch indexing and differentiates through it
+    (flash_attn_interface.py:533-581), so the exact gradient is the packed
+    sequences' gradient scattered back to the rows (and cache slots) it came
+    from, every other row zero.  The row map comes from the oracle's own
+    compaction applied to row indices."""
+    from flash_attn_triton import flash_attn_varlen_func
+    cu_q, cu_k = _cu(lq), _cu(lk)
+    q = randn((int(sum(lq)), hq, d), seed + 10, dtype)
+    if page is None:
+        k = randn((int(sum(lk)), hk, d), seed + 11, dtype)
+        v = randn((int(sum(lk)), hk, d), seed + 12, dtype)
+        bt = None
+    else:
+        k, v, bt = _pages(lk, page, hk, d, seed + 13, dtype)
+    uq = None if used_q is None else torch.tensor(used_q, dtype=torch.int32)
+    uk = None if used_k is None else torch.tensor(used_k, dtype=torch.int32)
+    mq = max(used_q) if used_q is not None else max(lq)
+    mk = max(used_k) if used_k is not None else max(lk)
+    rows_out = int(sum(used_q)) if used_q is not None else int(sum(lq))
+    do = randn((rows_out, hq, d), seed + 14, dtype)
+    dev = lambda t: None if t is None else t.to(DEV)
+    qd, kd, vd = (t.to(DEV).requires_grad_() for t in (q, k, v))
+    out = flash_attn_varlen_func(qd, kd, vd, dev(cu_q), dev(cu_k), mq, mk, causal=causal,
+                                 block_table=dev(bt), seqused_q=dev(uq), seqused_k=dev(uk), **kw)
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    bt_np = None if bt is None else bt.numpy()
+    cq, ck_, ckv, cu_q2, cu_k2 = ora.compact_varlen(to_np(q), to_np(k), to_np(v), cu_q.numpy(),
+                                                    cu_k.numpy(), used_q, used_k, bt_np)
+    qrow = np.arange(q.shape[0]).reshape(-1, 1, 1)
+    krow = np.arange(int(np.prod(k.shape[:-2]))).reshape(*k.shape[:-2], 1, 1)
+    qmap, kmap, _, _, _ = ora.compact_varlen(qrow, krow, krow, cu_q.numpy(), cu_k.numpy(),
+                                             used_q, used_k, bt_np)
+    grads = ora.attention_varlen_backward(cq, ck_, ckv, to_np(do), cu_q2, cu_k2,
+                                          kw.get("softmax_scale"), causal,
+                                          kw.get("window_size", (-1, -1)), kw.get("softcap", 0.0))
+    for name, t, g, rmap in (("dq", qd, grads[0], qmap), ("dk", kd, grads[1], kmap),
+                             ("dv", vd, grads[2], kmap)):
+        exact = np.zeros((int(np.prod(t.shape[:-2])),) + tuple(t.shape[-2:]))
+        exact[rmap[:, 0, 0]] = g
+        got = to_np(t.grad.cpu()).reshape(exact.shape)
+        err = np.abs(got - exact)
+        atol, rtol = (5e-3, 1e-2) if dtype == torch.float16 else (4e-2, 4e-2)
+        print(f"{name}: max-abs err {float(np.max(err)):.3e}")
+        assert np.all(np.isfinite(got)) and np.all(err <= atol + rtol * np.abs(exact)), (
+            f"{name}: max |err| {float(np.max(err)):.3e}")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_seqused_gradients(causal):
+    _grad_case([70, 300, 5, 257], [90, 300, 64, 260], d=64, causal=causal,
+               used_q=[33, 300, 0, 129], used_k=[90, 17, 64, 200], seed=21)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_paged_varlen_gradients(causal):
+    # Gradients land in the cache pages the block table names; spare pages
+    # and slots past each sequence stay zero.
+    _grad_case([5, 200, 64, 1], [37, 513, 64, 300], hq=8, hk=2, d=128, page=64,
+               causal=causal, seed=22)
+
+
+def test_paged_varlen_gradients_with_seqused_and_features():
+    _grad_case([40, 300, 2], [60, 500, 33], hq=8, hk=2, d=128, page=16, causal=True,
+               used_q=[40, 256, 1], used_k=[60, 301, 0], window_size=(96, 0), softcap=20.0,
+               softmax_scale=0.07, dtype=torch.bfloat16, seed=23)

@@ -278,7 +278,7 @@ def test_compact_varlen_seqused_is_truncated_per_sequence_sdpa():
 
 
 # ----------------------------------------------------------------- gradients
-def _torch_math(q, k, v, scale, causal, window, softcap, slopes, offset):
+def _torch_math(q, k, v, scale, causal, window, softcap, slopes, offset, bias=None):
     """The reference's math path (flash_attn_interface.py:15-49) in float64 torch,
     for autograd: BSHD inputs, GQA by repeat_interleave."""
     rep = q.shape[2] // k.shape[2]
@@ -289,6 +289,8 @@ def _torch_math(q, k, v, scale, causal, window, softcap, slopes, offset):
     kp = torch.arange(k.shape[1], dtype=torch.float64)[None, :]
     if slopes is not None:
         s = s - slopes[None, :, None, None] * (qp - kp).abs()
+    if bias is not None:
+        s = s + bias
     if softcap > 0:
         s = softcap * torch.tanh(s / softcap)
     keep = torch.ones_like(qp * kp, dtype=torch.bool)
@@ -324,6 +326,29 @@ def test_backward_matches_torch_autograd(case):
                                  case["softcap"], slopes, case["offset"])
     for g, t in zip(got, (tq, tk, tv)):
         np.testing.assert_allclose(g, t.grad.numpy(), atol=1e-12)
+
+
+@pytest.mark.parametrize("shape", [(2, 4, 7, 10), (1, 4, 7, 10), (2, 1, 1, 10), (7, 10),
+                                   (4, 1, 10)])
+def test_backward_bias_gradient_matches_torch_autograd(shape):
+    # attn_bias broadcast over batch / heads / rows: autograd sums dS over the
+    # broadcast dims; with softcap the bias sits inside the tanh.
+    rng = np.random.default_rng(52)
+    B, Sq, Sk, Hq, Hk, D = 2, 7, 10, 4, 2, 8
+    q = rng.standard_normal((B, Sq, Hq, D))
+    k = rng.standard_normal((B, Sk, Hk, D))
+    v = rng.standard_normal((B, Sk, Hk, D))
+    do = rng.standard_normal((B, Sq, Hq, D))
+    bias = rng.standard_normal(shape)
+    for causal, softcap in ((True, 0.0), (False, 4.0)):
+        tq, tk, tv, tb = (torch.from_numpy(x).requires_grad_() for x in (q, k, v, bias))
+        out = _torch_math(tq, tk, tv, 0.3, causal, (-1, -1), softcap, None, 3, tb)
+        out.backward(torch.from_numpy(do))
+        got = ora.attention_backward(q, k, v, do, 0.3, causal, (-1, -1), softcap, None, 3,
+                                     attn_bias=bias, return_dbias=True)
+        assert got[3].shape == bias.shape
+        for g, t in zip(got, (tq, tk, tv, tb)):
+            np.testing.assert_allclose(g, t.grad.numpy(), atol=1e-12)
 
 
 def test_backward_matches_finite_differences():
