@@ -187,8 +187,9 @@ int bwd_launch(const char* name, fa::BwdParams& p, int dtype, int64_t head_dim,
   p.window_right = clamp_window(window_right);
   const bool generic = alibi_slopes != nullptr || softcap > 0.f || p.drop.enabled ||
                        p.bias != nullptr || p.dbias != nullptr;
-  const hipError_t e = dtype == FA_DTYPE_F16 ? fa_launch_bwd_f16(p, (int)head_dim, generic, st)
-                                             : fa_launch_bwd_bf16(p, (int)head_dim, generic, st);
+  const hipError_t e = dtype == FA_DTYPE_F16   ? fa_launch_bwd_f16(p, (int)head_dim, generic, st)
+                       : dtype == FA_DTYPE_BF16 ? fa_launch_bwd_bf16(p, (int)head_dim, generic, st)
+                                                : fa_launch_bwd_f32(p, (int)head_dim, generic, st);
   return hip_status(e, name);
 }
 
@@ -198,11 +199,13 @@ int bwd_check_common(const char* name, const void* q, const void* k, const void*
                      int64_t head_dim, int64_t heads_q, int64_t heads_k) {
   if (!q || !k || !v || !out || !dout || !lse || !dq || !dk || !dv || !delta)
     return fail(FA_ERR_INVALID, "%s: null pointer argument", name);
-  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16)
-    return fail(FA_ERR_UNSUPPORTED, "%s: dtype %d not supported (fp16 / bf16)", name, dtype);
+  if (dtype != FA_DTYPE_F16 && dtype != FA_DTYPE_BF16 && dtype != FA_DTYPE_F32)
+    return fail(FA_ERR_UNSUPPORTED, "%s: dtype %d not supported (fp16 / bf16 / fp32)", name, dtype);
   if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(FA_ERR_UNSUPPORTED, "%s: head_dim %lld not in {32,64,128,256}", name,
                 (long long)head_dim);
+  if (dtype == FA_DTYPE_F32 && head_dim > 128)
+    return fail(FA_ERR_UNSUPPORTED, "%s: the fp32 backward supports head_dim 32, 64 and 128", name);
   if (heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0)
     return fail(FA_ERR_INVALID, "%s: bad head counts Hq=%lld Hk=%lld", name, (long long)heads_q,
                 (long long)heads_k);

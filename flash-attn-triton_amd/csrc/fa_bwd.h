@@ -49,3 +49,5 @@ struct BwdParams {
 // dQ (and delta) first, then dK / dV, both on `st`.  D in {32, 64, 128, 256}.
 hipError_t fa_launch_bwd_f16(const fa::BwdParams& p, int head_dim, bool generic, hipStream_t st);
 hipError_t fa_launch_bwd_bf16(const fa::BwdParams& p, int head_dim, bool generic, hipStream_t st);
+// fp32 (fa_bwd_f32.hip): D in {32, 64, 128}.
+hipError_t fa_launch_bwd_f32(const fa::BwdParams& p, int head_dim, bool generic, hipStream_t st);

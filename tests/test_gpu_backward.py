@@ -6,7 +6,8 @@ Bars: the reference's own gradient tests compare fp16 against SDPA at
 atol = rtol = 2e-2 (tests/test_compare_implementations.py:23-24,81-82).  Here
 the comparison is against the exact float64 gradient, elementwise
 |got - exact| <= GRAD_ATOL + GRAD_RTOL * |exact|: fp16 inputs carry P and dS
-rounded to fp16 into fp32 accumulations, bf16 rounds them 8x coarser.
+rounded to fp16 into fp32 accumulations, bf16 rounds them 8x coarser; fp32
+inputs keep every product in fp32 (the fp32 matrix core), within 1e-4.
 """
 import math
 
@@ -20,8 +21,8 @@ from oracle import attention as ora
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-GRAD_ATOL = {torch.float16: 5e-3, torch.bfloat16: 4e-2}
-GRAD_RTOL = {torch.float16: 1e-2, torch.bfloat16: 4e-2}
+GRAD_ATOL = {torch.float16: 5e-3, torch.bfloat16: 4e-2, torch.float32: 1e-4}
+GRAD_RTOL = {torch.float16: 1e-2, torch.bfloat16: 4e-2, torch.float32: 1e-4}
 
 
 def _check(name, got, exact, dtype):
@@ -207,11 +208,39 @@ def test_baseline_c2_sampled_heads():
 
 
 def test_forward_only_paths_raise_on_backward():
+    # fp32 at head dim 256 has no backward (its K^T / V^T registers would not fit).
     from flash_attn_triton import flash_attn_func
-    q = randn((1, 64, 2, 64), 100, torch.float32).to(DEV).requires_grad_()
+    q = randn((1, 64, 2, 256), 100, torch.float32).to(DEV).requires_grad_()
     out = flash_attn_func(q, q, q)
     with pytest.raises(NotImplementedError):
         out.sum().backward()
+
+
+@pytest.mark.parametrize("d", [16, 32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp32_head_dims(d, causal):
+    _dense_case(2, 150, 150, 4, 2, d, dtype=torch.float32, causal=causal, seed=140 + d)
+
+
+def test_fp32_cross_and_features():
+    _dense_case(1, 70, 301, 4, 2, 64, dtype=torch.float32, causal=True, seed=150)
+    _dense_case(2, 300, 300, 4, 2, 128, dtype=torch.float32, causal=True, window=(64, 0),
+                softcap=20.0, alibi=True, seed=151)
+    _dense_case(1, 190, 190, 2, 1, 32, dtype=torch.float32, causal=False, window=(16, 40),
+                softcap=5.0, seed=152, scale=0.3)
+
+
+def test_fp32_varlen():
+    _varlen_case([1, 130, 64, 257, 5], [3, 130, 200, 100, 5], Hq=4, Hk=2, D=64,
+                 dtype=torch.float32, causal=True, seed=160)
+    _varlen_case([300, 129, 64], [300, 129, 64], Hq=8, Hk=2, D=128, dtype=torch.float32,
+                 causal=True, window=(64, 0), softcap=30.0, alibi=True, seed=161)
+
+
+def test_fp32_bias_gradients():
+    _bias_case((1, 4, 120, 120), Sq=120, Sk=120, D=64, dtype=torch.float32, causal=True,
+               softcap=10.0, seed=170)
+    _bias_case((120, 120), Sq=120, Sk=120, D=128, dtype=torch.float32, causal=False, seed=171)
 
 
 def _bias_case(bias_shape, B=2, Sq=150, Sk=190, Hq=4, Hk=2, D=64, dtype=torch.float16,
