@@ -19,6 +19,33 @@ __device__ inline float round_half_away(float x) {
   return __builtin_truncf(x + __builtin_copysignf(0.5f, x));
 }
 
+// round_half_away(x) as an integer: the truncating convert of x +- 0.5 (the
+// same single fp32 addition, then the truncation the convert performs).
+__device__ inline int round_half_away_i(float x) {
+#pragma clang fp contract(off)
+  return (int)(x + __builtin_copysignf(0.5f, x));
+}
+
+// Low bytes of four ints in [-128, 127] as one dword (a in byte 0): two byte
+// permutes and a shift-or.
+__device__ inline uint32_t pack_i8x4_i(int a, int b, int c, int d) {
+  const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
+  return ab | (cd << 16);
+}
+
+// x / s of the Q quantizer (s = fp32(max(amax, 1)) / 127, |x| <= amax, x and
+// amax fp16 values) from inv = 1 / s (IEEE division, once per row): q0 = x inv
+// is within an ulp of x / s, and one correction with the exact remainder
+// x - q0 s gives the correctly rounded quotient (Markstein's theorem for a
+// correctly rounded reciprocal).  Checked equal to the IEEE division for every
+// such (x, amax) pair, 7.7e8 of them (tests/test_int8_division.py).
+__device__ inline float quant_div(float x, float s, float inv) {
+  const float q0 = x * inv;
+  const float r = __builtin_fmaf(-q0, s, x);
+  return __builtin_fmaf(r, inv, q0);
+}
+
 __device__ inline uint32_t pack_i8x4(float a, float b, float c, float d) {
   return ((uint32_t)(uint8_t)(int8_t)(int)a) | ((uint32_t)(uint8_t)(int8_t)(int)b << 8) |
          ((uint32_t)(uint8_t)(int8_t)(int)c << 16) | ((uint32_t)(uint8_t)(int8_t)(int)d << 24);

@@ -80,21 +80,6 @@ __device__ inline float group_max(float v) {
   return v;
 }
 
-// round_half_away(x) as an integer: the truncating convert of x +- 0.5 (the
-// same single fp32 addition, then the truncation the convert performs).
-__device__ inline int round_half_away_i(float x) {
-#pragma clang fp contract(off)
-  return (int)(x + __builtin_copysignf(0.5f, x));
-}
-
-// Low bytes of four ints in [-128, 127] as one dword (a in byte 0): two byte
-// permutes and a shift-or.
-__device__ inline uint32_t pack_i8x4_i(int a, int b, int c, int d) {
-  const uint32_t ab = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0c0c0400u);
-  const uint32_t cd = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0c0c0400u);
-  return ab | (cd << 16);
-}
-
 // The prepass for sequence lengths that are a multiple of 64 (every INT8
 // launch of the Python API): a workgroup quantizes 64 consecutive rows of one
 // (batch, head), whose addressing it computes once in scalar registers.  Four
@@ -261,14 +246,15 @@ void int8_fwd_kernel(const Int8Params p) {
     }
     amax = halves_max(amax);
     s_q = fmaxf(amax, 1.0f) / 127.0f;
+    const float inv_q = 1.0f / s_q;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) {
 #pragma unroll
       for (int wd = 0; wd < 4; ++wd) {
-        q8[kc][wd] = (int)pack_i8x4(round_half_away(qf[kc][4 * wd + 0] / s_q),
-                                    round_half_away(qf[kc][4 * wd + 1] / s_q),
-                                    round_half_away(qf[kc][4 * wd + 2] / s_q),
-                                    round_half_away(qf[kc][4 * wd + 3] / s_q));
+        q8[kc][wd] = (int)pack_i8x4_i(round_half_away_i(quant_div(qf[kc][4 * wd + 0], s_q, inv_q)),
+                                      round_half_away_i(quant_div(qf[kc][4 * wd + 1], s_q, inv_q)),
+                                      round_half_away_i(quant_div(qf[kc][4 * wd + 2], s_q, inv_q)),
+                                      round_half_away_i(quant_div(qf[kc][4 * wd + 3], s_q, inv_q)));
       }
     }
     __builtin_amdgcn_s_waitcnt(0x0f70);   // vmcnt(0): retire the Q loads before the loop

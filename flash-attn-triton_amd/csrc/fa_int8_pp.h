@@ -109,7 +109,8 @@ void int8_pp_kernel(const Int8Params p) {
 
   // ------------------------------------------------------------ Q8^T in VGPRs
   // Lane (c32, g) holds dims [32 kc + 16 g, +16) of row qi: the B operand of
-  // v_mfma_i32_32x32x32_i8.  Division form, bit-exact with the reference.
+  // v_mfma_i32_32x32x32_i8.  The quotient x / s_q is the IEEE division's
+  // (quant_div), bit-exact with the reference's division form.
   i32x4 q8[NKC];
   float row_scale;
   {
@@ -134,14 +135,15 @@ void int8_pp_kernel(const Int8Params p) {
     }
     amax = halves_max(amax);
     const float s_q = fmaxf(amax, 1.0f) / 127.0f;
+    const float inv_q = 1.0f / s_q;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) {
 #pragma unroll
       for (int wd = 0; wd < 4; ++wd) {
-        q8[kc][wd] = (int)pack_i8x4(round_half_away(qf[kc][4 * wd + 0] / s_q),
-                                    round_half_away(qf[kc][4 * wd + 1] / s_q),
-                                    round_half_away(qf[kc][4 * wd + 2] / s_q),
-                                    round_half_away(qf[kc][4 * wd + 3] / s_q));
+        q8[kc][wd] = (int)pack_i8x4_i(round_half_away_i(quant_div(qf[kc][4 * wd + 0], s_q, inv_q)),
+                                      round_half_away_i(quant_div(qf[kc][4 * wd + 1], s_q, inv_q)),
+                                      round_half_away_i(quant_div(qf[kc][4 * wd + 2], s_q, inv_q)),
+                                      round_half_away_i(quant_div(qf[kc][4 * wd + 3], s_q, inv_q)));
       }
     }
     row_scale = s_q * p.scale_log2;
@@ -404,8 +406,10 @@ void int8_pp_kernel(const Int8Params p) {
     load_k(j + NS - 1);
     load_v(j + NS - 2);
     softmax_tile(j, wave_masks(j));
-    // This wave's loads from the previous softmax step have landed.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(Tile::LPS));
+    // The loads of step j - 2 (K8 / s_k of tile j + 1, V of tile j), which
+    // the next GEMM phase reads, have landed; steps j - 1 and j stay in
+    // flight.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * Tile::LPS));
   };
   if (grp == 1) pp_barrier();
   if (J > 0) {
