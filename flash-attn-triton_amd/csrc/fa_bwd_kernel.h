@@ -449,6 +449,43 @@ void bwd_dq_kernel(const BwdParams p) {
   }
 }
 
+// Whole-row stores of 32 rows held in the accumulator layout (lane (c32, g):
+// dims 32 db + 8 (v / 4) + 4 g + v % 4 of row c32), times `scale`, packed to
+// 16 bits: the values go through `st` (32 rows of 2 D + 16 bytes, the pad
+// spreading a write's rows over the banks) and come back as 16-byte chunks of
+// whole rows, so each store instruction writes D / 8 lanes' worth of every
+// row it touches instead of 16 bytes of 32 rows.  (Stored directly, the dK /
+// dV rows of a non-causal launch, all finishing at once, reached HBM as
+// partial lines: 3.5x the bytes.)  Rows [0, rows_ok) are stored.
+template <class T, int D>
+__device__ inline void store_rows_staged(const f32x16* acc, float scale, uint8_t* st, int c32,
+                                         int g, int lane, uint16_t* row0, int64_t ss,
+                                         int rows_ok) {
+  constexpr int NDB = D / 32, PITCH = 2 * D + 16, CPR = D / 8, RPI = 64 / CPR;
+  uint8_t* const wr = st + c32 * PITCH + 8 * g;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      u32x2 val;
+      val[0] = T::pack2(acc[db][4 * r] * scale, acc[db][4 * r + 1] * scale);
+      val[1] = T::pack2(acc[db][4 * r + 2] * scale, acc[db][4 * r + 3] * scale);
+      *reinterpret_cast<u32x2*>(wr + (db * 4 + r) * 16) = val;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int rl = lane / CPR, cl = lane % CPR;
+  const uint8_t* const rd = st + rl * PITCH + cl * 16;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int r = RPI * i + rl;
+    const u32x4 x = *reinterpret_cast<const u32x4*>(rd + i * RPI * PITCH);
+    if (r < rows_ok) store16(row0 + (int64_t)r * ss + cl * 8, x);
+  }
+}
+
 // Q and dO tiles of BM rows stream through NS LDS stages, filled by LDS-DMA
 // buffer loads (no VGPR staging) issued NS - 1 tiles ahead; the LSE and delta
 // of the tile's rows ride along (one 4-byte-per-lane DMA each).
@@ -825,25 +862,24 @@ void bwd_dkdv_kernel(const BwdParams p) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   // ------------------------------------------------------------ dK = scale * dK^T, dV
-  if (!key_valid) return;
-  uint16_t* dkrow = static_cast<uint16_t*>(p.dk) + row_base(p, p.dk_sb, p.dk_ss, p.dk_sh, b, kvh, ks) +
-                    (int64_t)kj * p.dk_ss;
-  uint16_t* dvrow = static_cast<uint16_t*>(p.dv) + row_base(p, p.dv_sb, p.dv_ss, p.dv_sh, b, kvh, ks) +
-                    (int64_t)kj * p.dv_ss;
-#pragma unroll
-  for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = db * 32 + r * 8 + g * 4;
-      u32x2 vk, vv;
-      vk[0] = T::pack2(dk[db][4 * r] * p.scale, dk[db][4 * r + 1] * p.scale);
-      vk[1] = T::pack2(dk[db][4 * r + 2] * p.scale, dk[db][4 * r + 3] * p.scale);
-      vv[0] = T::pack2(dv[db][4 * r], dv[db][4 * r + 1]);
-      vv[1] = T::pack2(dv[db][4 * r + 2], dv[db][4 * r + 3]);
-      if (DO_DK) *reinterpret_cast<u32x2*>(dkrow + d) = vk;
-      if (DO_DV) *reinterpret_cast<u32x2*>(dvrow + d) = vv;
-    }
-  }
+  // Every wave's reads of the last tile are done once all waves pass the
+  // barrier: the stages then hold each wave's 32 rows of staging.
+  static_assert(4 * 32 * (2 * D + 16) <= Tile::LDS_BYTES, "output staging must fit the stages");
+  __syncthreads();
+  uint8_t* const st = smem_b + w * 32 * (2 * D + 16);
+  const int rows_ok = Sk - wk0;
+  if (DO_DK)
+    store_rows_staged<T, D>(dk, p.scale, st, c32, g, lane,
+                            static_cast<uint16_t*>(p.dk) +
+                                row_base(p, p.dk_sb, p.dk_ss, p.dk_sh, b, kvh, ks) +
+                                (int64_t)wk0 * p.dk_ss,
+                            p.dk_ss, rows_ok);
+  if (DO_DV)
+    store_rows_staged<T, D>(dv, 1.f, st, c32, g, lane,
+                            static_cast<uint16_t*>(p.dv) +
+                                row_base(p, p.dv_sb, p.dv_ss, p.dv_sh, b, kvh, ks) +
+                                (int64_t)wk0 * p.dv_ss,
+                            p.dv_ss, rows_ok);
 }
 
 }  // namespace fa
