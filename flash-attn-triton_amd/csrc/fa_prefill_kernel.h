@@ -137,8 +137,10 @@ void prefill_kernel(const FwdParams p) {
   const int qi = row0 + w * 32 + c32;
   const bool row_valid = qi < Sq;
   const int qpos = qi + (int)qoff;
+  // One slope per (batch, head): wave-uniform, also on rows past the
+  // sequence (their scores are discarded).
   float slope = 0.f;
-  if (GENERIC && p.alibi != nullptr && row_valid) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
+  if (GENERIC && p.alibi != nullptr) slope = p.alibi[(int64_t)b * p.alibi_sb + hh];
   const float* bias_row = nullptr;
   if (BIAS)
     bias_row = p.bias + (int64_t)b * p.bias_sb + (int64_t)hh * p.bias_sh + (int64_t)qi * p.bias_sq;
@@ -157,7 +159,10 @@ void prefill_kernel(const FwdParams p) {
   int key_hi = Sk - 1;
   if (causal) key_hi = min(key_hi, qp32);
   if (wr >= 0) key_hi = min(key_hi, qp32 + wr);
-  const int key_lo = wl >= 0 ? qp32 - wl : INT32_MIN;
+  // (-2^30 for no lower bound: positions stay below 2^29, so key_lo - n0
+  // cannot overflow.)
+  constexpr int kNoKey = 1 << 30;
+  const int key_lo = wl >= 0 ? qp32 - wl : -kNoKey;
 
   // Key range [k_lo, k_hi) any row of the workgroup can see.
   int k_hi = Sk;
@@ -242,24 +247,28 @@ void prefill_kernel(const FwdParams p) {
   // of its group reads key row 16cc + 4g + j/4 (+8), dims 16(c32/16) + 4(j%4).
   const int vt_lane = (4 * g + (lane & 15) / 4) * VSTR + 16 * (c32 >> 4) + 4 * (lane & 3);
 
-  // Per-wave tile classification: skipped (no key of the tile visible to any
-  // row of this wave) or masked (some key hidden from some row).
-  auto wave_skips = [&](int t) {
-    const int n0 = t * BN, n1 = n0 + BN;
-    bool skip = !wave_active || n0 >= Sk;
-    if (causal) skip = skip || n0 > qpos_w_max;
-    if (wr >= 0) skip = skip || n0 > qpos_w_max + wr;
-    if (wl >= 0) skip = skip || n1 - 1 < qpos_w_min - wl;
-    return skip;
-  };
-  auto wave_masks = [&](int t) {
-    const int n0 = t * BN, n1 = n0 + BN;
-    bool need = n1 > Sk;
-    if (causal) need = need || n1 - 1 > qpos_w_min;
-    if (wr >= 0) need = need || n1 - 1 > qpos_w_min + wr;
-    if (wl >= 0) need = need || n0 < qpos_w_max - wl;
-    return need;
-  };
+  // Per-wave tile classification from key bounds computed once (integers,
+  // so the per-tile tests stay on the scalar unit): a tile is skipped when no
+  // key of it lies in [kw_lo, kw_hi], the union of this wave's rows' visible
+  // ranges, and needs the lower / upper mask when it reaches below kf_lo /
+  // above kf_hi, their intersection.
+  int kw_lo = 0, kw_hi = Sk - 1, kf_lo = 0, kf_hi = Sk - 1;
+  if (causal) {
+    kw_hi = min(kw_hi, qpos_w_max);
+    kf_hi = min(kf_hi, qpos_w_min);
+  }
+  if (wr >= 0) {
+    kw_hi = min(kw_hi, qpos_w_max + wr);
+    kf_hi = min(kf_hi, qpos_w_min + wr);
+  }
+  if (wl >= 0) {
+    kw_lo = max(kw_lo, qpos_w_min - wl);
+    kf_lo = qpos_w_max - wl;
+  }
+  if (!wave_active) {
+    kw_lo = kNoKey;
+    kw_hi = -kNoKey;
+  }
 
   f32x16 acc[NDB];
 #pragma unroll
@@ -293,16 +302,46 @@ void prefill_kernel(const FwdParams p) {
       }
     }
   };
+  // Score transform of the generic epilogue without attn_bias (D < 256):
+  // every score first becomes t = x k, x = s scale - slope |qpos - key| the
+  // scaled score with ALiBi and k = 2 log2(e) / softcap with softcap (log2(e)
+  // without).  The row max is taken on t (the cap is increasing) and softcap
+  // enters with the exponent,
+  //   softcap log2(e) tanh(x / softcap) = c2 - 2 c2 / (1 + 2^t),  c2 = softcap log2(e),
+  // so the exp2 argument is one FMA: (c2 - m) - 2 c2 / (1 + 2^t).
+  // ALiBi: on tiles whose keys are at or before every row's position (all
+  // of them under causal masking: the keys past it are masked),
+  // -k slope |qpos - key| = A - akk with A = ak (qpos - n0 - 4g - 32 kb) per
+  // lane and 32-key block, ak = -k slope, and akk = ak koff per score slot
+  // (koff < 32 the slot's key offset in the block, the same in every lane):
+  // one FMA and one add per score.  (The 8-wave D = 128 tiles have no
+  // registers left for akk and take the |qpos - key| form.)
+  constexpr bool kFastT = GENERIC && !BIAS && D < 256;
+  constexpr bool kAkk = kFastT && (NKB == 1 || D <= 64);
+  const bool alibi_on = GENERIC && p.alibi != nullptr;
+  const bool cap_on = kFastT && p.softcap > 0.f;
+  const float tk = GENERIC ? p.scale * (p.softcap > 0.f ? p.softcap_k : kLog2e) : 1.f;
+  const float ak = GENERIC ? -slope * (p.softcap > 0.f ? p.softcap_k : kLog2e) : 0.f;
+  const float c2 = p.softcap * kLog2e, m2c2 = -2.f * c2;
+  auto koff = [](int kb, int v) __attribute__((always_inline)) { return kb * 32 + 8 * (v >> 2) + (v & 3); };
+  float akk[kAkk ? 16 : 1];
+  if constexpr (kAkk) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) akk[v] = ak * (float)koff(0, v);
+  }
+
   // Softmax of one tile of scores starting at key n0: GENERIC transform,
-  // boundary mask, lazy max / rescale, P = exp2(s - m) packed to the element
-  // type as the B operand of pv (pb[cc] holds keys 16cc .. 16cc + 15 in the
-  // MFMA's k order), row sums.
-  auto softmax_tile = [&](f32x16* sc, int n0, bool masked, u32x4* pb) {
+  // boundary masks (keys below key_lo when mlo, above key_hi when mhi), lazy
+  // max / rescale, P = exp2(s - m) packed to the element type as the B
+  // operand of pv (pb[cc] holds keys 16cc .. 16cc + 15 in the MFMA's k
+  // order), row sums.
+  auto softmax_tile = [&](f32x16* sc, int n0, bool mlo, bool mhi, u32x4* pb) {
     // GENERIC: scale, ALiBi and softcap, scores -> log2 units.  Otherwise the
     // scores stay raw (scale > 0) and the scale is folded into the exp2
     // argument and the max.
-    // D = 256 keeps the direct form: its registers are already at the limit.
-    if (GENERIC && (BIAS || D >= 256)) {
+    // With attn_bias or D = 256 the transform is applied in full here (those
+    // kernels are at their register limit).
+    if (GENERIC && !kFastT) {
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
@@ -319,70 +358,50 @@ void prefill_kernel(const FwdParams p) {
           sc[kb][v] = x * kLog2e;
         }
       }
-    } else if (GENERIC) {
-      // The same transform with its constants folded per tile (this epilogue
-      // is VALU-bound): qpos - key = dq0 - koff with dq0 = qpos - n0 - 4g and
-      // koff = 32 kb + 8 (v / 4) + v % 4 fixed per slot, and with softcap only
-      // x k = x (2 log2 e / softcap) is needed:
-      //   softcap log2(e) tanh(x / softcap) = c2 - 2 c2 / (1 + 2^(x k)),
-      //   x k = s (scale k) - (slope k) |qpos - key|,  c2 = softcap log2(e).
-      const int dq0 = qp32 - n0 - 4 * g;
-      const bool alibi = p.alibi != nullptr;
-      // |qpos - key| as a float: an integer subtract of the slot's offset (an
-      // inline constant below 64) and one convert.
-      auto dist = [&](int kb, int v) { return fabsf((float)(dq0 - (kb * 32 + 8 * (v >> 2) + (v & 3)))); };
-      if (p.softcap > 0.f) {
-        const float sk = p.scale * p.softcap_k, ak = -slope * p.softcap_k;
-        const float c2 = p.softcap * kLog2e, m2c2 = -2.f * c2;
-        auto cap = [&](float xk) {
-          return fmaf(m2c2, __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(xk)), c2);
-        };
-        // (One 32-key block at a time: interleaving the exp / rcp chains of
-        // several blocks buys nothing and costs registers.)
-        if (alibi) {
+    } else if (kFastT) {
+      if (alibi_on) {
+        const int dq0 = qp32 - n0 - 4 * g;   // qpos - key = dq0 - koff
+        if (kAkk && (causal || n0 + BN - 1 <= qpos_w_min)) {
 #pragma unroll
           for (int kb = 0; kb < NKB; ++kb) {
+            const float A = ak * (float)(dq0 - 32 * kb);
 #pragma unroll
-            for (int v = 0; v < 16; ++v)
-              sc[kb][v] = cap(fmaf(ak, dist(kb, v), sc[kb][v] * sk));
-            __builtin_amdgcn_sched_barrier(0);
+            for (int v = 0; v < 16; ++v) sc[kb][v] = fmaf(sc[kb][v], tk, A) - akk[kAkk ? v : 0];
           }
         } else {
 #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb) {
+          for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) sc[kb][v] = cap(sc[kb][v] * sk);
-            __builtin_amdgcn_sched_barrier(0);
-          }
+            for (int v = 0; v < 16; ++v)
+              sc[kb][v] = fmaf(ak, fabsf((float)(dq0 - koff(kb, v))), sc[kb][v] * tk);
         }
       } else {
-        const float sl2 = p.scale * kLog2e, al2 = -slope * kLog2e;
-        if (alibi) {
 #pragma unroll
-          for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-              sc[kb][v] = fmaf(al2, dist(kb, v), sc[kb][v] * sl2);
-        } else {
-#pragma unroll
-          for (int kb = 0; kb < NKB; ++kb)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) sc[kb][v] *= sl2;
-        }
+        for (int kb = 0; kb < NKB; ++kb) sc[kb] *= tk;
       }
     }
-    // Boundary tiles only (a wave-uniform branch): keys outside
-    // [key_lo, key_hi] -> -inf.
-    if (masked) {
+    // Boundary tiles only (wave-uniform branches): keys outside
+    // [key_lo, key_hi] -> -inf, one compare per bound against the slot's key
+    // offset (an inline constant).
+    auto mask_tile = [&](auto lo_c, auto hi_c) __attribute__((always_inline)) {
+      const int mbase = n0 + 4 * g;
+      const int lo_rel = key_lo - mbase, hi_rel = key_hi - mbase;
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int key = n0 + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3);
-          if (key < key_lo || key > key_hi) sc[kb][v] = -INFINITY;
+          const int ko = koff(kb, v);
+          const bool hide = (decltype(lo_c)::value && ko < lo_rel) || (decltype(hi_c)::value && ko > hi_rel);
+          if (hide) sc[kb][v] = -INFINITY;
         }
       }
-    }
+    };
+    if (D >= 256 ? (mlo || mhi) : (mlo && mhi))
+      mask_tile(std::true_type{}, std::true_type{});
+    else if (mlo)
+      mask_tile(std::true_type{}, std::false_type{});
+    else if (mhi)
+      mask_tile(std::false_type{}, std::true_type{});
     // Row max over this lane's scores: four independent max3 chains.
     float mq[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
@@ -395,7 +414,9 @@ void prefill_kernel(const FwdParams p) {
       }
     }
     const float sl = GENERIC ? 1.f : p.scale_log2;
-    const float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * sl;
+    float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * sl;
+    if (cap_on && mx != -INFINITY)
+      mx = fmaf(m2c2, __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(mx)), c2);
     const bool raise = mx > m_run + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(raise)) {
       const float m_new = raise ? mx : m_run;
@@ -406,43 +427,71 @@ void prefill_kernel(const FwdParams p) {
       m_run = m_new;
     }
     const float m_use = m_run == -INFINITY ? 0.f : m_run;
-    float lq[4] = {0.f, 0.f, 0.f, 0.f};   // independent partial row sums
-    if (GENERIC && p.drop.enabled) {
-      // Dropout: the row sums take the undropped P, the product the dropped
-      // one (one Philox call per 16 keys of this lane's row).
+    // P and the row sums.  With softcap (a uniform branch) the exp2
+    // arguments are formed in place first: the cap, then - m; a masked score
+    // stays -inf.
+    auto finish = [&](auto cap_c) __attribute__((always_inline)) {
+      constexpr bool CAP = decltype(cap_c)::value;
+      if constexpr (CAP) {
+        const float c2m = c2 - m_use;
+        auto cap_arg = [&](auto masked_c) __attribute__((always_inline)) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const float x = sc[kb][v];
+              const float y = fmaf(m2c2, __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(x)), c2m);
+              sc[kb][v] = decltype(masked_c)::value && x == -INFINITY ? -INFINITY : y;
+            }
+        };
+        if (mlo || mhi)
+          cap_arg(std::true_type{});
+        else
+          cap_arg(std::false_type{});
+      }
+      auto expo = [&](float x) __attribute__((always_inline)) { return CAP ? x : fmaf(x, sl, -m_use); };
+      float lq[4] = {0.f, 0.f, 0.f, 0.f};   // independent partial row sums
+      if (GENERIC && p.drop.enabled) {
+        // Dropout: the row sums take the undropped P, the product the dropped
+        // one (one Philox call per 16 keys of this lane's row).
+#pragma unroll
+        for (int cc = 0; cc < NCC; ++cc) {
+          const f32x16& sv = sc[cc >> 1];
+          const int o8 = (cc & 1) * 8;
+          const u32x4 r = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float e0 = __builtin_amdgcn_exp2f(expo(sv[o8 + 2 * j]));
+            const float e1 = __builtin_amdgcn_exp2f(expo(sv[o8 + 2 * j + 1]));
+            lq[j] += e0 + e1;
+            pb[cc][j] = T::pack2(e0 * dropout_factor(p.drop, r, 2 * j),
+                                 e1 * dropout_factor(p.drop, r, 2 * j + 1));
+          }
+        }
+        l_run += (lq[0] + lq[1]) + (lq[2] + lq[3]);
+        return;
+      }
 #pragma unroll
       for (int cc = 0; cc < NCC; ++cc) {
         const f32x16& sv = sc[cc >> 1];
         const int o8 = (cc & 1) * 8;
-        const u32x4 r = dropout_draws(p.drop, (n0 >> 4) + cc, g, qi, hh, b);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
-          const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
-          lq[j] += e0 + e1;
-          pb[cc][j] = T::pack2(e0 * dropout_factor(p.drop, r, 2 * j),
-                               e1 * dropout_factor(p.drop, r, 2 * j + 1));
+          const float e0 = __builtin_amdgcn_exp2f(expo(sv[o8 + 2 * j]));
+          const float e1 = __builtin_amdgcn_exp2f(expo(sv[o8 + 2 * j + 1]));
+          pb[cc][j] = T::pack2(e0, e1);
+          if (T::kSumRounded)
+            lq[j] = T::sum2(pb[cc][j], lq[j]);
+          else
+            lq[j] += e0 + e1;
         }
       }
       l_run += (lq[0] + lq[1]) + (lq[2] + lq[3]);
-      return;
-    }
-#pragma unroll
-    for (int cc = 0; cc < NCC; ++cc) {
-      const f32x16& sv = sc[cc >> 1];
-      const int o8 = (cc & 1) * 8;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], sl, -m_use));
-        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], sl, -m_use));
-        pb[cc][j] = T::pack2(e0, e1);
-        if (T::kSumRounded)
-          lq[j] = T::sum2(pb[cc][j], lq[j]);
-        else
-          lq[j] += e0 + e1;
-      }
-    }
-    l_run += (lq[0] + lq[1]) + (lq[2] + lq[3]);
+    };
+    if (kFastT && cap_on)
+      finish(std::integral_constant<bool, kFastT>{});
+    else
+      finish(std::false_type{});
   };
 
   // ------------------------------------------------------------ main loop
@@ -465,9 +514,10 @@ void prefill_kernel(const FwdParams p) {
       load_k(t + 1);
       load_v(t + 1);
     }
-    if (!wave_skips(t)) {
+    const int n0 = t * BN;
+    if (n0 <= kw_hi && n0 + BN - 1 >= kw_lo) {
       qk(k_slot(it), s);
-      softmax_tile(s, t * BN, wave_masks(t), pbuf);
+      softmax_tile(s, n0, n0 < kf_lo, n0 + BN - 1 > kf_hi, pbuf);
       pv(v_slot(it), pbuf);
     }
     if (has_next) {
