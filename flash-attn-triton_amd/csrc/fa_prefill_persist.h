@@ -168,20 +168,29 @@ void prefill_persist_kernel(const FwdParams p) {
   uint8_t* const v_lds = smem_ps + NS * TILEB;
   const uint32_t k_lds_a = lds_address(k_lds) + IPW * w * 1024;
   const uint32_t v_lds_a = lds_address(v_lds) + IPW * w * 1024;
-  const int Sk = p.seqlen_k;
+  // Every tile of this kernel's blocks is full (the host launches it only
+  // for whole row blocks and key lengths a multiple of the block), so a
+  // tile's resource covers its own rows; the next block's K / V bases (n_k,
+  // n_v) are set once per block, which keeps the per-tile address work to a
+  // few scalar instructions.
+  const uint32_t k_tile_ext = rows_extent(0, BN, p.k_ss, D);
+  const uint32_t v_tile_ext = rows_extent(0, BN, p.v_ss, D);
+  int64_t n_k = 0, n_v = 0;
+  auto set_next = [&]() __attribute__((always_inline)) {
+    if (r_cur + 1 < rounds) {
+      int64_t a0, a1, a2;
+      int r0, j0;
+      make_blk(r_cur + 1, a0, a1, a2, n_k, n_v, r0, j0);
+    }
+  };
   auto load_tile = [&](int jj, int stage, bool is_k) __attribute__((always_inline)) {
     const bool in_cur = jj < c_J;
-    int64_t nb_q, nb_o, nb_l, nb_k = 0, nb_v = 0;
-    int nb_row0, nb_J;
-    const bool nxt = !in_cur && r_cur + 1 < rounds;
-    if (nxt) make_blk(r_cur + 1, nb_q, nb_o, nb_l, nb_k, nb_v, nb_row0, nb_J);
-    const bool live = in_cur || nxt;
+    const bool live = in_cur || r_cur + 1 < rounds;
     const int j = in_cur ? jj : jj - c_J;
-    const int64_t base = is_k ? (in_cur ? c_k : nb_k) : (in_cur ? c_v : nb_v);
+    const int64_t base = is_k ? (in_cur ? c_k : n_k) : (in_cur ? c_v : n_v);
     const int64_t ss = is_k ? p.k_ss : p.v_ss;
-    const int n0 = j * BN;
-    const uint32_t ext = live ? rows_extent(n0, Sk, ss, D) : 0u;
-    const u32x4 rs = make_rsrc_words((is_k ? kg : vg) + (live ? base + (int64_t)n0 * ss : 0), ext);
+    const uint32_t ext = live ? (is_k ? k_tile_ext : v_tile_ext) : 0u;
+    const u32x4 rs = make_rsrc_words((is_k ? kg : vg) + base + (int64_t)(j * BN) * ss, ext);
     const uint32_t dst = (is_k ? k_lds_a : v_lds_a) + stage * TILEB;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, is_k ? k_off[i] : v_off[i]);
@@ -400,6 +409,7 @@ void prefill_persist_kernel(const FwdParams p) {
     make_blk(0, q0, o0, l0, c_k, c_v, c_row0, c_J);
     load_q_rows(q0, c_row0);
   }
+  set_next();
 #pragma unroll
   for (int r = 0; r < NS - 1; ++r) load_tile(r, r, true);
 #pragma unroll
@@ -458,6 +468,7 @@ void prefill_persist_kernel(const FwdParams p) {
     pp_barrier();
     ++r_cur;
     make_blk(r_cur, c_q, t64, t64, c_k, c_v, c_row0, c_J);
+    set_next();
     set_rows();
     load_q_rows(c_q, c_row0);
 #pragma unroll
