@@ -458,26 +458,35 @@ void prefill_persist_kernel(const FwdParams p) {
     int64_t c_q, c_o, c_l;
     make_blk(r_cur, c_q, c_o, c_l, c_k, c_v, c_row0, c_J);
     const int lane_s = opaque(lane);
-    stage_rows_store<T, NDB>(acc, inv_l, st_o, lane_s & 31, lane_s >> 5, lane_s,
-                             og + c_o + (int64_t)(c_row0 + 32 * rb) * p.o_ss, p.o_ss, 32);
-    if (p.lse != nullptr && g == 0) p.lse[c_l + (int64_t)qi * p.lse_ss] = lse_val;
-    if (r_cur + 1 >= rounds) break;
+    u32x4 orows[8];
+    stage_rows_gather<T, NDB>(acc, inv_l, st_o, lane_s & 31, lane_s >> 5, lane_s, orows);
+    uint16_t* const orow0 = og + c_o + (int64_t)(c_row0 + 32 * rb) * p.o_ss;
+    float* const lse_p = p.lse != nullptr ? p.lse + c_l + (int64_t)qi * p.lse_ss : nullptr;
+    if (r_cur + 1 >= rounds) {
+      stage_rows_put(orows, orow0, p.o_ss, lane_s);
+      if (lse_p != nullptr && g == 0) *lse_p = lse_val;
+      break;
+    }
     // Next block: its Q rows into the Q staging areas once every wave has
-    // read its output rows back.  The output stores and the Q rows are in
-    // flight together; the wait covers both.
+    // read its output rows back, then the output stores (issued after the Q
+    // rows, so that the wait below covers the Q rows and not the stores).
     pp_barrier();
     ++r_cur;
     make_blk(r_cur, c_q, t64, t64, c_k, c_v, c_row0, c_J);
     set_next();
     set_rows();
     load_q_rows(c_q, c_row0);
+    stage_rows_put(orows, orow0, p.o_ss, lane_s);
+    if (lse_p != nullptr && g == 0) *lse_p = lse_val;
 #pragma unroll
     for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
     m_run = -INFINITY;
     l_run = 0.f;
     m_c = 0.f;
     cneg = f32x16{};
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    // At most the 8 output stores and the LSE store outstanding: the Q rows
+    // have landed.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(8));
     pp_barrier();
   }
 }
