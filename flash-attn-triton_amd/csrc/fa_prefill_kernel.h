@@ -206,36 +206,40 @@ void prefill_kernel(const FwdParams p) {
     v_off[i] = c < CHUNKS ? (uint32_t)(c / CPR) * v_row_b + (uint32_t)(c % CPR) * 16 : 0xfffffff0u;
   }
 
-  u32x4 kreg[KPT], vreg[KPT];
-  auto load_k = [&](int t) {
+  // Register staging of the tile loads: one set (the next tile) or, for the
+  // generic 4-wave tiles, two (the next two tiles: a load has two tiles of
+  // compute to land in; these kernels wait on load latency otherwise).
+  constexpr bool kDeep = GENERIC && NW == 4 && D <= 128;
+  u32x4 kreg[KPT], vreg[KPT], kreg2[kDeep ? KPT : 1], vreg2[kDeep ? KPT : 1];
+  auto load_k = [&](int t, u32x4* kr) {
     const int n0 = t * BN;
     const auto rs = make_rsrc(kg + (int64_t)n0 * p.k_ss, rows_extent(n0, Sk, p.k_ss, D));
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) kreg[i] = buf_load16(rs, k_off[i], 0);
+    for (int i = 0; i < KPT; ++i) kr[i] = buf_load16(rs, k_off[i], 0);
   };
-  auto load_v = [&](int t) {
+  auto load_v = [&](int t, u32x4* vr) {
     const int n0 = t * BN;
     const auto rs = make_rsrc(vg + (int64_t)n0 * p.v_ss, rows_extent(n0, Sk, p.v_ss, D));
 #pragma unroll
-    for (int i = 0; i < KPT; ++i) vreg[i] = buf_load16(rs, v_off[i], 0);
+    for (int i = 0; i < KPT; ++i) vr[i] = buf_load16(rs, v_off[i], 0);
   };
   // LDS: [K slot 0][K slot 1][V slot 0][V slot 1].
   auto k_slot = [&](int i) { return smem + (i & 1) * KTILE; };
   auto v_slot = [&](int i) { return smem + 2 * KTILE + (i & 1) * VTILE; };
-  auto store_k = [&](int slot) {
+  auto store_k = [&](int slot, const u32x4* kr) {
     uint16_t* Ks = k_slot(slot);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int c = tid + i * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) store16(Ks + (c / CPR) * KSTR + (c % CPR) * 8, kreg[i]);
+      if (CHUNKS % NT == 0 || c < CHUNKS) store16(Ks + (c / CPR) * KSTR + (c % CPR) * 8, kr[i]);
     }
   };
-  auto store_v = [&](int slot) {
+  auto store_v = [&](int slot, const u32x4* vr) {
     uint16_t* Vs = v_slot(slot);
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int c = tid + i * NT;
-      if (CHUNKS % NT == 0 || c < CHUNKS) store16(Vs + (c / CPR) * VSTR + (c % CPR) * 8, vreg[i]);
+      if (CHUNKS % NT == 0 || c < CHUNKS) store16(Vs + (c / CPR) * VSTR + (c % CPR) * 8, vr[i]);
     }
   };
 
@@ -500,29 +504,58 @@ void prefill_kernel(const FwdParams p) {
   // next tile's loads in flight; LDS slot i & 1 holds K_i and V_i.
   u32x4 pbuf[NCC];
   f32x16 s[NKB];
-  if (J > 0) {
-    load_k(t_begin);
-    load_v(t_begin);
-    store_k(0);
-    store_v(0);
-  }
-  for (int it = 0; it < J; ++it) {
-    const int t = t_begin + it;
-    __syncthreads();
-    const bool has_next = it + 1 < J;
-    if (has_next) {
-      load_k(t + 1);
-      load_v(t + 1);
-    }
-    const int n0 = t * BN;
+  auto compute = [&](int it) __attribute__((always_inline)) {
+    const int n0 = (t_begin + it) * BN;
     if (n0 <= kw_hi && n0 + BN - 1 >= kw_lo) {
       qk(k_slot(it), s);
       softmax_tile(s, n0, n0 < kf_lo, n0 + BN - 1 > kf_hi, pbuf);
       pv(v_slot(it), pbuf);
     }
-    if (has_next) {
-      store_k(it + 1);
-      store_v(it + 1);
+  };
+  if (J > 0) {
+    load_k(t_begin, kreg);
+    load_v(t_begin, vreg);
+    store_k(0, kreg);
+    store_v(0, vreg);
+  }
+  if constexpr (kDeep) {
+    // Tile it + 1 waits in one register set while tile it + 2 loads into the
+    // other; the sets alternate, so the loop runs tiles in pairs.
+    if (J > 1) {
+      load_k(t_begin + 1, kreg2);
+      load_v(t_begin + 1, vreg2);
+    }
+    auto step = [&](int it, u32x4* st_k, u32x4* st_v, u32x4* ld_k, u32x4* ld_v)
+        __attribute__((always_inline)) {
+      __syncthreads();
+      if (it + 2 < J) {
+        load_k(t_begin + it + 2, ld_k);
+        load_v(t_begin + it + 2, ld_v);
+      }
+      compute(it);
+      if (it + 1 < J) {
+        store_k(it + 1, st_k);
+        store_v(it + 1, st_v);
+      }
+    };
+    for (int it = 0; it < J; it += 2) {
+      step(it, kreg2, vreg2, kreg, vreg);
+      if (it + 1 < J) step(it + 1, kreg, vreg, kreg2, vreg2);
+    }
+  } else {
+    for (int it = 0; it < J; ++it) {
+      const int t = t_begin + it;
+      __syncthreads();
+      const bool has_next = it + 1 < J;
+      if (has_next) {
+        load_k(t + 1, kreg);
+        load_v(t + 1, vreg);
+      }
+      compute(it);
+      if (has_next) {
+        store_k(it + 1, kreg);
+        store_v(it + 1, vreg);
+      }
     }
   }
 
