@@ -1,6 +1,6 @@
 """Benchmark of the gfx950 FlashAttention-2 forward (one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--prewarm SECONDS] [--workload NAME]
 
 A "step" is one call of the public entry point on one batch of synthetic
 input already resident in HBM.  The default workload is BASELINE config 2,
@@ -15,6 +15,11 @@ prepass included), ``decode`` (config 4, paged GQA decode through
 FLOP convention (reference README.md:226-229): causal 2*B*H*D*S*(S+1),
 non-causal 4*B*H*D*S^2; varlen counts 4*H*D per unmasked (q, k) pair; decode
 is measured in algorithmic bytes (K/V rows read + q + out + block table).
+
+Before the W warmup steps every measurement runs untimed steps for
+``--prewarm`` seconds (default 0.5) so that the timed steps see settled GPU
+clocks; the line reports how many (``prewarm_steps``).  The timed region is
+exactly K steps either way.
 
 The JSON line carries ``roofline`` and ``cpu_baseline``.  ``roofline.achieved``
 is the algorithmic work of one launch divided by the mean duration of the
@@ -413,7 +418,8 @@ def _pmc_pass(workload, counter, kernels, outdir):
     d = os.path.join(outdir, f"{workload}_{counter}")
     cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "pmc", "--",
            sys.executable, os.path.abspath(__file__), "--workload", workload, "--steps", "2",
-           "--warmup", "1", "--cpu-budget", "0", "--traffic", "off", "--extras", "off"]
+           "--warmup", "1", "--prewarm", "0", "--cpu-budget", "0", "--traffic", "off",
+           "--extras", "off"]
     subprocess.run(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=180,
                    check=True)
     found = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
@@ -490,10 +496,27 @@ class _LaunchTimer:
         return sum(ms) / len(ms) / 1e3 if ms else None
 
 
-def measure(torch, wl, steps, warmup):
-    """Whole-job time of ``steps`` steps after ``warmup`` untimed ones, and the
-    mean launch time of the dominant kernel inside the timed region."""
+def prewarm(torch, step, seconds):
+    """Untimed steps for about ``seconds`` of wall time, in batches of 8 with a
+    synchronization after each, before the counted warmup: the GPU's clocks
+    take on the order of 100 ms of continuous load to settle (the C2 causal
+    launch measured 660 us after 3 warmup steps, 571 us after 30 and 546 us
+    after 200 on one MI355X)."""
+    n, t0 = 0, time.perf_counter()
+    while seconds > 0 and time.perf_counter() - t0 < seconds and n < 100000:
+        for _ in range(8):
+            step()
+        n += 8
+        torch.cuda.synchronize()
+    return n
+
+
+def measure(torch, wl, steps, warmup, prewarm_s=0.0):
+    """Whole-job time of ``steps`` steps after the clock pre-warm and ``warmup``
+    untimed steps, and the mean launch time of the dominant kernel inside the
+    timed region."""
     step = wl["step"]
+    n_pre = prewarm(torch, step, prewarm_s)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -514,6 +537,7 @@ def measure(torch, wl, steps, warmup):
         "avg_launch_s": avg_launch_s,
         "achieved": achieved,
         "frac": achieved / wl["peak"],
+        "prewarm_steps": n_pre,
     }
 
 
@@ -534,6 +558,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--prewarm", type=float, default=0.5,
+                    help="seconds of untimed steps before the warmup steps, for the GPU clocks "
+                         "to settle (0 = none)")
     ap.add_argument("--workload", default="dense_causal", choices=sorted(WORKLOADS))
     ap.add_argument("--cpu-budget", type=float, default=8.0,
                     help="seconds of host work for each CPU baseline sample (0 = skip)")
@@ -564,7 +591,7 @@ def main():
     import torch
     torch.backends.cuda.matmul.allow_tf32 = False
     wl = WORKLOADS[args.workload](torch)
-    m = measure(torch, wl, args.steps, args.warmup)
+    m = measure(torch, wl, args.steps, args.warmup, args.prewarm)
     cpu = run_cpu(torch, wl, args.cpu_budget)
 
     roof = {
@@ -593,6 +620,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm_steps": m["prewarm_steps"],
         "ms_per_step": round(m["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -610,11 +638,12 @@ def main():
         runs = {"dense_causal": m}
         for name in EXTRAS:
             xw = WORKLOADS[name](torch)
-            xm = measure(torch, xw, args.steps, args.warmup)
+            xm = measure(torch, xw, args.steps, args.warmup, args.prewarm)
             runs[name] = xm
             extra[name] = {
                 "metric": xw["metric"], "value": round(xm["value"], 3), "unit": xw["unit"],
-                "ms_per_step": round(xm["ms_per_step"], 4), "dtype": xw["dtype"],
+                "ms_per_step": round(xm["ms_per_step"], 4), "prewarm_steps": xm["prewarm_steps"],
+                "dtype": xw["dtype"],
                 "config": xw["config"],
                 "roofline": {"bound": xw["bound"], "achieved": round(xm["achieved"], 3),
                              "peak": round(xw["peak"], 1), "unit": xw["peak_unit"],
