@@ -189,6 +189,24 @@ void int8_pp_kernel(const Int8Params p) {
     const u32x4 rs = make_rsrc_words(skg + (live ? n0 : 0), left * 4);
     buf_load4_lds(rs, sk_lds_a + (rel % NS) * SKB, sk_voff);
   };
+  // The same for a tile the caller knows is whole and inside the key range
+  // (no selects, fixed extents).
+  const uint32_t v_tile_ext = rows_extent(0, BN, p.v_ss, D);
+  auto load_k_full = [&](int rel) {
+    const int n0 = rel * BN;
+    const u32x4 rk = make_rsrc_words(k8g + (int64_t)n0 * D, (uint32_t)(BN * D));
+    const uint32_t dst = k_lds_a + (rel % NS) * KTILEB;
+#pragma unroll
+    for (int i = 0; i < KIPW; ++i) buf_load16_lds(rk, dst + i * 1024, k_off[i]);
+    const u32x4 rs = make_rsrc_words(skg + n0, (uint32_t)(BN * 4));
+    buf_load4_lds(rs, sk_lds_a + (rel % NS) * SKB, sk_voff);
+  };
+  auto load_v_full = [&](int rel) {
+    const u32x4 rs = make_rsrc_words(vg + (int64_t)(rel * BN) * p.v_ss, v_tile_ext);
+    const uint32_t dst = v_lds_a + (rel % NS) * VTILEB;
+#pragma unroll
+    for (int i = 0; i < VIPW; ++i) buf_load16_lds(rs, dst + i * 1024, v_off[i]);
+  };
   auto load_v = [&](int rel) {
     const int n0 = rel * BN;
     const uint32_t ext = rel < J ? rows_extent(n0, Sk, p.v_ss, D) : 0u;
@@ -411,13 +429,33 @@ void int8_pp_kernel(const Int8Params p) {
     // flight.
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * Tile::LPS));
   };
+  // Steps j < j_full: tile j is unmasked for every wave of the workgroup
+  // and the tiles loaded (K8 j + 3, V j + 2) are live, whole and inside the
+  // key range.
+  auto softmax_step_full = [&](int j) {
+    load_k_full(j + NS - 1);
+    load_v_full(j + NS - 2);
+    softmax_tile(j, false);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * Tile::LPS));
+  };
+  int j_full = min(J - (NS - 1), Sk / BN - (NS - 1));
+  if (causal) j_full = min(j_full, (row0 + qoff + 1) / BN);
   if (grp == 1) pp_barrier();
   if (J > 0) {
     gemm(0, 0, yes{}, no{});
     pp_barrier();
-    softmax_step(0);
+    if (j_full > 0)
+      softmax_step_full(0);
+    else
+      softmax_step(0);
     pp_barrier();
-    for (int j = 1; j < J; ++j) {
+    for (int j = 1; j < j_full; ++j) {
+      gemm(j % NS, (j - 1) % NS, yes{}, yes{});
+      pp_barrier();
+      softmax_step_full(j);
+      pp_barrier();
+    }
+    for (int j = j_full > 1 ? j_full : 1; j < J; ++j) {
       gemm(j % NS, (j - 1) % NS, yes{}, yes{});
       pp_barrier();
       softmax_step(j);
