@@ -420,14 +420,23 @@ void int8_pp_kernel(const Int8Params p) {
   // with a barrier after each step, group 1 one barrier behind group 0.
   using yes = std::true_type;
   using no = std::false_type;
+  // The wait that ends a softmax step.  Tile t's rows (K8, s_k of tile t,
+  // V of tile t - 1) are loaded by both groups in their softmax step t - 3,
+  // and the first GEMM to read them, group 0's GEMM(t), follows group 0's
+  // softmax step t - 1 and group 1's softmax step t - 2 (group 1 runs one
+  // phase behind): group 0 waits for its loads of two steps back, group 1
+  // for those of one step back.
+  auto step_wait = [&]() {
+    if (grp == 0)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * Tile::LPS));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(Tile::LPS));
+  };
   auto softmax_step = [&](int j) {
     load_k(j + NS - 1);
     load_v(j + NS - 2);
     softmax_tile(j, wave_masks(j));
-    // The loads of step j - 2 (K8 / s_k of tile j + 1, V of tile j), which
-    // the next GEMM phase reads, have landed; steps j - 1 and j stay in
-    // flight.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * Tile::LPS));
+    step_wait();
   };
   // Steps j < j_full: tile j is unmasked for every wave of the workgroup
   // and the tiles loaded (K8 j + 3, V j + 2) are live, whole and inside the
@@ -436,7 +445,7 @@ void int8_pp_kernel(const Int8Params p) {
     load_k_full(j + NS - 1);
     load_v_full(j + NS - 2);
     softmax_tile(j, false);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * Tile::LPS));
+    step_wait();
   };
   int j_full = min(J - (NS - 1), Sk / BN - (NS - 1));
   if (causal) j_full = min(j_full, (row0 + qoff + 1) / BN);

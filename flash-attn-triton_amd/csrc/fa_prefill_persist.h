@@ -364,9 +364,10 @@ void prefill_persist_kernel(const FwdParams p) {
   };
 
   // The next block's Q rows into L2 (one 4-byte load per 128-byte line, 64
-  // lines per wave, written past the rings as a throwaway).  It is issued
-  // after the phase's tile loads, so the next phase's wait, two phases
-  // later, covers it without delaying this phase's own wait.
+  // lines per wave, written as a throwaway into the last 2 KiB past the
+  // rings, which no output staging uses).  It is issued after the phase's
+  // tile loads, and the step waits leave it in flight until the tile loads
+  // issued after it are waited for.
   auto prefetch_q = [&]() __attribute__((always_inline)) {
     int64_t n_q, n_o, n_l, n_k, n_v;
     int n_row0, n_J;
@@ -374,14 +375,30 @@ void prefill_persist_kernel(const FwdParams p) {
     const uint16_t* q0 = qg + n_q + (int64_t)(n_row0 + 32 * rb) * p.q_ss;
     const u32x4 rs = make_rsrc_words(q0, rows_extent(0, 32, p.q_ss, D));
     const uint32_t voff = (uint32_t)(lane >> 1) * (uint32_t)(p.q_ss * 2) + (uint32_t)(lane & 1) * 128;
-    buf_load4_lds(rs, lds_address(smem_ps + Tile::STAGE_OFF + w * 256), voff);
+    buf_load4_lds(rs, lds_address(smem_ps + Tile::STAGE_OFF + 4 * 8192 - 8 * 256 + w * 256), voff);
   };
+
+  // The wait that ends a softmax step.  Tile t's rows are loaded by both
+  // groups in their softmax step t - 3, and the first GEMM to read them,
+  // group 0's GEMM(t), follows group 0's softmax step t - 1 and group 1's
+  // softmax step t - 2 (group 1 runs one phase behind): group 0 waits for
+  // its loads of two steps back, group 1 for those of one step back.  E
+  // loads issued after those (a Q prefetch, the next block's Q rows) stay
+  // in flight too.
+  auto step_wait = [&](auto e_c) __attribute__((always_inline)) {
+    constexpr int E = decltype(e_c)::value;
+    if (grp == 0)
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * IPW + E));
+    else
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * IPW + E));
+  };
+  using e0c = std::integral_constant<int, 0>;
+  using e1c = std::integral_constant<int, 1>;
 
   // Softmax phase of the current block's tile j: the tile loads of K_{j+3}
   // and V_{j+2} (the next block's first tiles past the end), the softmax,
-  // then a wait for the loads of step j-2 (K_{j+1}, V_j), which the next
-  // GEMM phase reads; the loads of steps j-1 and j (and the Q prefetch of
-  // either) stay in flight.
+  // then the step wait (the Q prefetch of this step or the one before stays
+  // in flight).
   auto softmax_step = [&](int j) __attribute__((always_inline)) {
     load_tile(j + NS - 1, (j + NS - 1) % NS, true, std::false_type{});
     load_tile(j + NS - 2, (j + NS - 2) % NS, false, std::false_type{});
@@ -390,9 +407,9 @@ void prefill_persist_kernel(const FwdParams p) {
     if (pre) prefetch_q();
     softmax_tile(j);
     if ((pre || (j > 0 && j == c_J - 3)) && more)
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * IPW + 1));
+      step_wait(e1c{});
     else
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * IPW));
+      step_wait(e0c{});
   };
 
   // The same for a phase j < J - 4: both tiles are this block's, no Q
@@ -401,7 +418,7 @@ void prefill_persist_kernel(const FwdParams p) {
     load_tile(j + NS - 1, (j + NS - 1) % NS, true, std::true_type{});
     load_tile(j + NS - 2, (j + NS - 2) % NS, false, std::true_type{});
     softmax_tile(j);
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * IPW));
+    step_wait(e0c{});
   };
 
   // A block's Q rows straight into the Q registers: lane (c32, g) loads dims
@@ -412,6 +429,26 @@ void prefill_persist_kernel(const FwdParams p) {
     const uint16_t* qrow = qg + q_base + (int64_t)(row0 + 32 * rb + c32) * p.q_ss + 8 * g;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) qreg[kc] = *reinterpret_cast<const u32x4*>(qrow + 16 * kc);
+  };
+
+  // The block's last softmax phase.  The Q registers are free from here on
+  // (the block's last S^T product is done), so the next block's Q rows go
+  // into them first, ahead of the phase's tile loads, and the phase's own
+  // wait leaves them in flight with those tile loads.
+  auto softmax_step_last = [&](int j, bool more) __attribute__((always_inline)) {
+    if (more) {
+      int64_t n_q, n_o, n_l, n_k2, n_v2;
+      int n_row0, n_J;
+      make_blk(r_cur + 1, n_q, n_o, n_l, n_k2, n_v2, n_row0, n_J);
+      load_q_regs(n_q, n_row0);
+    }
+    load_tile(j + NS - 1, (j + NS - 1) % NS, true, std::false_type{});
+    load_tile(j + NS - 2, (j + NS - 2) % NS, false, std::false_type{});
+    softmax_tile(j);
+    if (more)
+      step_wait(std::integral_constant<int, NKC>{});
+    else
+      step_wait(e0c{});
   };
 
   // ------------------------------------------------------------ prologue
@@ -438,11 +475,63 @@ void prefill_persist_kernel(const FwdParams p) {
   pp_barrier();
 
   uint16_t* const og = static_cast<uint16_t*>(p.o);
+  // Output of block r, whose state is still in acc / l_run / m_run: staged
+  // through the LDS area st_o (kStageOutBytes) and stored as whole rows,
+  // with the block's LSE.
+  auto finish_block = [&](int r, uint8_t* st_o) __attribute__((always_inline)) {
+    const float l_tot = halves_sum(l_run);
+    const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float lse_val = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+    int64_t f_q, f_o, f_l, f_k, f_v;
+    int f_row0, f_J;
+    make_blk(r, f_q, f_o, f_l, f_k, f_v, f_row0, f_J);
+    const int lane_s = opaque(lane);
+    u32x4 orows[8];
+    stage_rows_gather<T, NDB>(acc, inv_l, st_o, lane_s & 31, lane_s >> 5, lane_s, orows);
+    const int row_w = f_row0 + 32 * rb;
+    stage_rows_put(orows, og + f_o + (int64_t)row_w * p.o_ss, p.o_ss, lane_s);
+    if (p.lse != nullptr && g == 0) p.lse[f_l + (int64_t)(row_w + c32) * p.lse_ss] = lse_val;
+  };
+  auto reset_state = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+    m_run = -INFINITY;
+    l_run = 0.f;
+    m_c = 0.f;
+    cneg = f32x16{};
+  };
+  // Output staging areas.  Group 0 stages in the phase of its last O^T
+  // product (group 1 is in its last softmax phase, whose tile loads fill K
+  // stage 2 and V stage 1): K stage 3 and V stage 2 hold tiles that both
+  // groups have finished reading, and the area past the rings is free.
+  // Group 1 stages one phase after its last O^T product, while group 0's
+  // first softmax phase of the next block loads K stage 3 and V stage 2:
+  // it uses V stage 3 (its own last O^T operand, next loaded two phases
+  // later) and the area past the rings.  The Q-row prefetch writes its
+  // throwaway bytes at the end of that area, clear of both.
+  static_assert(kStageOutBytes <= TILEB && 3 * kStageOutBytes <= 4 * 8192 - 8 * 256,
+                "output staging must fit the stages and the area past the rings");
+  uint8_t* const past = smem_ps + Tile::STAGE_OFF;
+  uint8_t* const st_own = grp == 0
+      ? (sid == 0 ? k_lds + 3 * TILEB : sid == 1 ? v_lds + 2 * TILEB : past + (sid - 2) * kStageOutBytes)
+      : (sid == 0 ? v_lds + 3 * TILEB : past + (sid - 1) * kStageOutBytes);
+
+  // The block loop.  Group 1 runs one phase behind group 0 for the whole
+  // life of the workgroup; nothing drains between blocks.  Per block each
+  // group runs GEMM(0) (S^T only), softmax(0), ..., softmax(J-1) and
+  // GEMM(J) (O^T only), one barrier after each, 2J + 1 phases.  The next
+  // block's Q rows go into the Q registers at the start of softmax(J-1).  Group 0 stages its
+  // output right after its GEMM(J); group 1 does so after the barrier that
+  // ends its GEMM(J), i.e. in its next phase, before its GEMM(0) of the
+  // next block.  So group 1's GEMM(J) shares a phase with group 0's next
+  // GEMM(0) (16 + 16 MFMAs per SIMD, a full GEMM phase), and each group's
+  // output stores and Q loads run beside the other group's work.
+  if (grp == 1) pp_barrier();
   for (;;) {
     // ---------------------------------------------------------- one block
     const int J = c_J;
     const int j_tail = J - 4;   // the phases from J - 4 on prefetch Q rows or wait for them
-    if (grp == 1) pp_barrier();
+    const bool more = r_cur + 1 < rounds;
     gemm(0, 0, yes{}, no{});
     pp_barrier();
     if (j_tail > 0)
@@ -456,63 +545,34 @@ void prefill_persist_kernel(const FwdParams p) {
       softmax_step_plain(j);
       pp_barrier();
     }
-    for (int j = j_tail > 1 ? j_tail : 1; j < J; ++j) {
+    for (int j = j_tail > 1 ? j_tail : 1; j < J - 1; ++j) {
       gemm(j % NS, (j - 1) % NS, yes{}, yes{});
       pp_barrier();
       softmax_step(j);
       pp_barrier();
     }
-    gemm(0, (J - 1) % NS, no{}, yes{});
+    gemm((J - 1) % NS, (J - 2) % NS, yes{}, yes{});
     pp_barrier();
+    softmax_step_last(J - 1, more);
+    pp_barrier();
+    gemm(0, (J - 1) % NS, no{}, yes{});
+    // Group 1 passes the barrier that ends this phase before its output,
+    // group 0 after it: one barrier each.  Both scale the next block's Q
+    // rows in their next phase, where the wait for them also covers the
+    // tile loads of two phases back (the loads complete in order).
+    if (grp == 1) pp_barrier();
+    finish_block(r_cur, st_own);
+    reset_state();
     if (grp == 0) pp_barrier();
-
-    // ---------------------------------------------------------- block change
-    // Every LDS read of the block is done (group 1's last GEMM phase ended
-    // at the barrier just passed) and the tile loads still in flight fill K
-    // stages 0-2 and V stages 0-1 with the next block's first tiles, so K
-    // stage 3, V stages 2-3 and the area past the rings (80 KiB) are free:
-    // the output goes through them (wave 0 in K stage 3, the others from V
-    // stage 2 on), stored as whole rows.  The next block's Q rows are loaded
-    // into the Q registers first (this block's last S^T product is done),
-    // so their latency runs under the output staging.  No barrier is needed
-    // before the next block: the next writes into these areas are the tile
-    // loads of its softmax phase 0, after a barrier that every wave reaches
-    // only past its staging reads.
-    const bool more = r_cur + 1 < rounds;
-    if (more) {
-      int64_t n_q, n_o, n_l, n_k2, n_v2;
-      int n_row0, n_J;
-      make_blk(r_cur + 1, n_q, n_o, n_l, n_k2, n_v2, n_row0, n_J);
-      load_q_regs(n_q, n_row0);
-    }
-    const float l_tot = halves_sum(l_run);
-    const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const float lse_val = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
-    static_assert(kStageOutBytes <= TILEB && 7 * kStageOutBytes <= 2 * TILEB + 4 * 8192,
-                  "output staging must fit K stage 3 and V stages 2-3 plus the area past the rings");
-    uint8_t* const st_o = w == 0 ? k_lds + 3 * TILEB : v_lds + 2 * TILEB + (w - 1) * kStageOutBytes;
-    int64_t c_q, c_o, c_l;
-    make_blk(r_cur, c_q, c_o, c_l, c_k, c_v, c_row0, c_J);
-    const int lane_s = opaque(lane);
-    u32x4 orows[8];
-    stage_rows_gather<T, NDB>(acc, inv_l, st_o, lane_s & 31, lane_s >> 5, lane_s, orows);
-    uint16_t* const orow0 = og + c_o + (int64_t)(c_row0 + 32 * rb) * p.o_ss;
-    float* const lse_p = p.lse != nullptr ? p.lse + c_l + (int64_t)qi * p.lse_ss : nullptr;
-    stage_rows_put(orows, orow0, p.o_ss, lane_s);
-    if (lse_p != nullptr && g == 0) *lse_p = lse_val;
     if (!more) break;
+    prescale_q();
     ++r_cur;
-    make_blk(r_cur, c_q, t64, t64, c_k, c_v, c_row0, c_J);
+    make_blk(r_cur, t64, t64, t64, c_k, c_v, c_row0, c_J);
     set_next();
     set_rows();
-#pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
-    m_run = -INFINITY;
-    l_run = 0.f;
-    m_c = 0.f;
-    cneg = f32x16{};
-    prescale_q();
   }
+  // Group 0 matches group 1's last barrier.
+  if (grp == 0) pp_barrier();
 }
 
 }  // namespace fa
