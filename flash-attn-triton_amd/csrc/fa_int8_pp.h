@@ -14,7 +14,7 @@
 // O^T += V_{j-1}^T P_{j-1} on v_mfma_f32_32x32x16_f16: 8 + 16 MFMAs per wave
 // and 64-key tile, against 16 + 16 with fp16 scores) and a softmax phase,
 // separated by workgroup barriers, so each SIMD's matrix core is fed by one
-// of its two waves while the other converts, scales and exponentiates.
+// of its two waves while the other exponentiates.
 //
 // LDS, four stages per operand, filled by the buffer loads' LDS mode:
 //   K8 tile : 64 rows x 128 B; 16-byte chunk c of row r at c ^ ((r >> 1) & 7),
@@ -252,18 +252,24 @@ void int8_pp_kernel(const Int8Params p) {
   float m_run = -INFINITY;   // running (possibly stale) max, log2 units
   float m_c = 0.f;           // finite max P is taken against
   float l_run = 0.f;
-  f32x16 s[NKB];             // scores i32 * s_k[key] of the current tile
+  // Exponents of the current tile, i32 * s_k[key] * s_q * scale * log2(e) - m_c.
+  f32x16 s[NKB];
   u32x4 pbuf[NCC];
+  // B operand of the coefficient product below: this lane's row scale in
+  // k-slot 0 (lanes 0-31), zero in k-slot 1 (lanes 32-63).
+  const float coef_b = g == 0 ? row_scale : 0.f;
 
   constexpr int NQK = NKC * NKB;
   constexpr int NPV = NDB * NCC;
   // One GEMM phase: S^T = K8 Q8^T from K stage kst (DO_QK) and
   // O^T += V^T P^T from V stage vst (DO_PV), operand reads running ahead of
-  // the products as in prefill_pp_kernel.  The wave then converts its own
-  // int32 scores and multiplies them by the key scales of stage kst: that
-  // VALU work sits under the PV products, where a wave hides a few VALU
-  // instructions behind each of its own MFMAs, instead of in the softmax
-  // phase, where every VALU instruction slows the other wave's products.
+  // the products as in prefill_pp_kernel.  The wave then turns its own
+  // int32 scores into exponents, fma(i32, coef, -m_c) with the per-(key, row)
+  // coefficients from two fp32 outer products: that VALU work sits under
+  // the PV products, where a wave hides a few VALU instructions behind each
+  // of its own MFMAs, instead of in the softmax phase, where every VALU
+  // instruction slows the other wave's products, and the softmax phase is
+  // left with the max, exp2, packing and row sums of the fp16 kernel.
   auto gemm = [&](int kst, int vst, auto do_qk_c, auto do_pv_c) {
     constexpr bool DO_QK = decltype(do_qk_c)::value;
     constexpr bool DO_PV = decltype(do_pv_c)::value;
@@ -274,18 +280,19 @@ void int8_pp_kernel(const Int8Params p) {
     const uint8_t* Vs = v_lds + vst * VTILEB;
     const float* skl = reinterpret_cast<const float*>(sk_lds + kst * SKB);
     u32x4 ka[DO_QK ? NQK : 1];
-    f32x4 sk4[DO_QK ? 4 * NKB : 1];
+    float ska[DO_QK ? NKB : 1];
     u32x4 va[DO_PV ? NPV : 1];
     i32x16 si[DO_QK ? NKB : 1];
+    f32x16 coef[DO_QK ? NKB : 1];
     // Region 1: the S^T chain (or, without it, the whole O^T update).
     if constexpr (DO_QK) {
 #pragma unroll
       for (int i = 0; i < NQK; ++i)
         ka[i] = *reinterpret_cast<const u32x4*>(Ks + k_ofs[i / NKB] + (i % NKB) * 32 * KROWB);
-      // Key scales of this lane's accumulator rows kb*32 + 8 r + 4 g + [0, 4).
+      // A operand of the coefficient product: key kb*32 + c32's scale (the
+      // same in both k-slots; the B operand's slot 1 is zero).
 #pragma unroll
-      for (int i = 0; i < 4 * NKB; ++i)
-        sk4[i] = *reinterpret_cast<const f32x4*>(skl + (i >> 2) * 32 + (i & 3) * 8 + g * 4);
+      for (int kb = 0; kb < NKB; ++kb) ska[kb] = skl[kb * 32 + c32];
     }
     if constexpr (DO_PV) {
 #pragma unroll
@@ -300,14 +307,21 @@ void int8_pp_kernel(const Int8Params p) {
         for (int kb = 0; kb < NKB; ++kb)
           si[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, ka[kc * NKB + kb]),
                                                          q8[kc], si[kb], 0, 0, 0);
+      // coef[kb] = s_k[key] * (s_q * scale * log2 e) for every (key, row) of
+      // the S^T accumulator, as the outer product of the key scales and the
+      // row scales on the fp32 matrix core (exact products, one rounding).
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        coef[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(ska[kb], coef_b, f32x16{}, 0, 0, 0);
       // Scheduling groups (0x100 = LDS read, 0x008 = MFMA, 0x002 = VALU).
-      constexpr int NRD1 = NQK + 4 * NKB + (DO_PV ? 2 * NVA0 : 0);
+      constexpr int NRD1 = NQK + NKB + (DO_PV ? 2 * NVA0 : 0);
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
       for (int i = 0; i < NQK; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         __builtin_amdgcn_sched_group_barrier(0x100, (NRD1 - 8 + NQK - 1) / NQK, 0);
       }
+      __builtin_amdgcn_sched_group_barrier(0x008, NKB, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
     // Region 2: the O^T update with the remaining V^T reads, and the
@@ -328,7 +342,7 @@ void int8_pp_kernel(const Int8Params p) {
       for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          float t = (float)si[kb][v] * sk4[kb * 4 + (v >> 2)][v & 3];
+          float t = fmaf((float)si[kb][v], coef[kb][v], -m_c);
           asm volatile("" : "+v"(t));
           s[kb][v] = t;
         }
@@ -351,9 +365,9 @@ void int8_pp_kernel(const Int8Params p) {
     __builtin_amdgcn_s_setprio(0);
   };
 
-  // Softmax of tile rel: boundary mask, lazy max / O rescale,
-  // P = exp2(s * s_q * scale * log2 e - m_c) packed as the B operand of pv,
-  // row sums over the rounded P.
+  // Softmax of tile rel: boundary mask, lazy max / O rescale (the exponents
+  // move with m_c), P = exp2(s) packed as the B operand of pv, row sums
+  // over the rounded P.
   auto softmax_tile = [&](int rel, bool masked) {
     if (masked) {
       const int hi0 = key_hi - rel * BN - 4 * g;
@@ -378,7 +392,7 @@ void int8_pp_kernel(const Int8Params p) {
           mq[q] = fmaxf(fmaxf(mq[q], s[kb][v + 2 * q]), s[kb][v + 2 * q + 1]);
       }
     }
-    const float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * row_scale;
+    const float mx = halves_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) + m_c;
     const bool raise = mx > m_run + kRescaleSlack;
     if (__builtin_amdgcn_ballot_w64(raise)) {
       const float m_new = raise ? mx : m_run;
@@ -387,7 +401,11 @@ void int8_pp_kernel(const Int8Params p) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
       m_run = m_new;
-      m_c = m_run == -INFINITY ? 0.f : m_run;
+      const float m_use = m_run == -INFINITY ? 0.f : m_run;
+      const float shift = m_use - m_c;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) s[kb] -= shift;
+      m_c = m_use;
     }
     float lq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -396,8 +414,8 @@ void int8_pp_kernel(const Int8Params p) {
       const int o8 = (cc & 1) * 8;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float e0 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j], row_scale, -m_c));
-        const float e1 = __builtin_amdgcn_exp2f(fmaf(sv[o8 + 2 * j + 1], row_scale, -m_c));
+        const float e0 = __builtin_amdgcn_exp2f(sv[o8 + 2 * j]);
+        const float e1 = __builtin_amdgcn_exp2f(sv[o8 + 2 * j + 1]);
         pbuf[cc][j] = F16::pack2(e0, e1);
         lq[j] = F16::sum2(pbuf[cc][j], lq[j]);
       }
