@@ -137,7 +137,10 @@ struct BwdDqTile {
   static constexpr int TILEB = BN * D * 2;       // bytes of one K or V stage
   static constexpr int IPS = TILEB / 1024;       // 1-KiB DMA instructions per K (or V) stage
   static constexpr int IPW = 2 * IPS / NW;       // per wave: waves [0, NW/2) load K, the rest V
-  static constexpr int LDS_BYTES = NS * 2 * TILEB;
+  // The prologue stages each wave's 32 Q and dO rows (then its O rows) in
+  // LDS before the K / V stages take it over.
+  static constexpr int ROWS_B = 64 * D;          // bytes of 32 rows
+  static constexpr int LDS_BYTES = NS * 2 * TILEB > 2 * NW * ROWS_B ? NS * 2 * TILEB : 2 * NW * ROWS_B;
   static_assert(IPW * NW == 2 * IPS && IPW > 0, "K and V tiles must split evenly over the waves");
 };
 
@@ -214,28 +217,56 @@ void bwd_dq_kernel(const BwdParams p) {
   const int J = t_end - t_begin;
 
   // ------------------------------------------------------------ Q, dO rows; delta
+  // The wave's 32 rows of Q and dO, then of O, go global -> LDS as whole
+  // rows (LDS-DMA, 1 KiB of consecutive rows per instruction, the K / V
+  // tile layout) and come back in the MFMA operand layout.  Read straight
+  // in that layout (16 bytes of 32 rows per instruction, each 128-byte line
+  // touched by four instructions) the rows were fetched from HBM about twice
+  // (measured on MI355X: 792 MB for 402 MB of Q, dO and O at B=4 H=32
+  // S=4096 D=128).  Rows past the sequence read as zeros.
   u32x4 qreg[NKC], doreg[NKC];
   float dsum = 0.f;
   {
-    const uint16_t* qrow = static_cast<const uint16_t*>(p.q) +
-                           row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hh, qs) + (int64_t)qi * p.q_ss;
-    const uint16_t* drow = static_cast<const uint16_t*>(p.dout) +
-                           row_base(p, p.do_sb, p.do_ss, p.do_sh, b, hh, qs) + (int64_t)qi * p.do_ss;
-    const uint16_t* orow = static_cast<const uint16_t*>(p.o) +
-                           row_base(p, p.o_sb, p.o_ss, p.o_sh, b, hh, qs) + (int64_t)qi * p.o_ss;
+    constexpr int NI = D / 16;   // 1-KiB DMA instructions per 32 rows
+    uint8_t* const st_a = smem_b + w * Tile::ROWS_B;
+    uint8_t* const st_b = smem_b + (NW + w) * Tile::ROWS_B;
+    int sr[NI], sc[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) swz_inverse<D>(4 * i + (lane >> 4), lane & 15, sr[i], sc[i]);
+    auto stage = [&](const void* t, int64_t sb, int64_t ss, int64_t sh, uint8_t* st) {
+      const uint16_t* rows = static_cast<const uint16_t*>(t) + row_base(p, sb, ss, sh, b, hh, qs) +
+                             (int64_t)wrow0 * ss;
+      const u32x4 rs = make_rsrc_words(rows, rows_extent(wrow0, Sq, ss, D));
+      const uint32_t dst = lds_address(st);
+#pragma unroll
+      for (int i = 0; i < NI; ++i)
+        buf_load16_lds(rs, dst + i * 1024, (uint32_t)sr[i] * (uint32_t)(ss * 2) + (uint32_t)sc[i] * 16);
+    };
+    auto read = [&](const uint8_t* st, u32x4* out) {
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc)
+        out[kc] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(st) +
+                                                  swz_off<D>(c32, 2 * kc + g));
+    };
+    stage(p.q, p.q_sb, p.q_ss, p.q_sh, st_a);
+    stage(p.dout, p.do_sb, p.do_ss, p.do_sh, st_b);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    read(st_a, qreg);
+    read(st_b, doreg);
+    // The Q reads have returned before the O rows overwrite their area.
+    __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+    stage(p.o, p.o_sb, p.o_ss, p.o_sh, st_a);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    u32x4 oreg[NKC];
+    read(st_a, oreg);
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) {
-      const int d = kc * 16 + g * 8;
-      const u32x4 z = {0, 0, 0, 0};
-      qreg[kc] = row_valid ? load16(qrow + d) : z;
-      doreg[kc] = row_valid ? load16(drow + d) : z;
-      const u32x4 o4 = row_valid ? load16(orow + d) : z;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        dsum = fmaf(T::to_float((uint16_t)(o4[e] & 0xffffu)),
+        dsum = fmaf(T::to_float((uint16_t)(oreg[kc][e] & 0xffffu)),
                     T::to_float((uint16_t)(doreg[kc][e] & 0xffffu)), dsum);
-        dsum = fmaf(T::to_float((uint16_t)(o4[e] >> 16)), T::to_float((uint16_t)(doreg[kc][e] >> 16)),
-                    dsum);
+        dsum = fmaf(T::to_float((uint16_t)(oreg[kc][e] >> 16)),
+                    T::to_float((uint16_t)(doreg[kc][e] >> 16)), dsum);
       }
     }
   }
@@ -257,8 +288,10 @@ void bwd_dq_kernel(const BwdParams p) {
     if (g == 0) p.delta[lse_base + (int64_t)qi * p.lse_ss] = delta;
   }
   // Retire these loads before the DMA stream starts (the compiler does not
-  // count the DMA instructions).
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // count the DMA instructions), and every wave's staging reads before the
+  // K / V stages overwrite the staging areas.
+  __builtin_amdgcn_s_waitcnt(0x0070);   // vmcnt(0) lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
 
   // ------------------------------------------------------------ DMA stream
   // Waves [0, NW/2) copy K tiles, the others V tiles; lane l writes chunk
