@@ -173,7 +173,7 @@ void bwd_dq_kernel(const BwdParams p) {
   int mb, id;
   if (!VARLEN ||
       !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_blocks, p.group, p.causal != 0, mb, id))
-    work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, mb, id);
+    work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kBwdCausalSpan, mb, id);
   const int hh = id % p.heads_q;
   const int b = id / p.heads_q;
   const int kvh = hh / p.group;
@@ -566,7 +566,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
   int nb, id;
   if (!VARLEN ||
       !work_item_kv_rr(blockIdx.x, p.total_blocks, p.n_blocks, 1, p.causal != 0, nb, id))
-    work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kCausalSpan, nb, id);
+    work_item(blockIdx.x, p.total_blocks, p.n_blocks, p.causal != 0, kBwdCausalSpan, nb, id);
   if (p.causal) nb = p.n_blocks - 1 - nb;
   const int kvh = id % p.heads_k;
   const int b = id / p.heads_k;

@@ -176,10 +176,15 @@ __device__ inline bool work_item_kv_rr(int L, int total, int n_mblocks, int grou
   return true;
 }
 
-// work_item span of the causal launches of the ping-pong forward, INT8 and
-// backward kernels: 4 groups measured best on MI355X at B=4 H=32 S=4096 (1:
-// 5-7% slower, all groups of an XCD: 1-3% slower).
+// work_item span of the causal launches of the ping-pong forward and INT8
+// kernels (and of the fp32 backward): 4 groups measured best on MI355X at
+// B=4 H=32 S=4096 (1: 5-7% slower, all groups of an XCD: 1-3% slower).
 constexpr int kCausalSpan = 4;
+// The 16-bit backward kernels' span: each group streams 2 MiB of K / V (dQ)
+// or Q / dO (dK/dV) per XCD at that shape, so four groups at a time
+// overflowed the 4 MiB L2 (causal dQ + dK/dV read 1882 MB for 672 MB of
+// inputs); two read 1333 MB for 0.9% more time, one 1367 MB for 5.4%.
+constexpr int kBwdCausalSpan = 2;
 
 __device__ inline u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ inline void store16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }

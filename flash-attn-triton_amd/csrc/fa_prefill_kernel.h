@@ -29,6 +29,7 @@
 #pragma once
 
 #include "fa_fwd_kernel.h"
+#include "fa_stage_rows.h"
 
 namespace fa {
 
@@ -563,6 +564,22 @@ void prefill_kernel(const FwdParams p) {
   const float l_tot = halves_sum(l_run);
   const float inv_l = l_tot > 0.f ? 1.f / l_tot : 0.f;
   const float lse_val = l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : -INFINITY;
+  if constexpr (D == 128) {
+    // The output goes through LDS (the tile area, once every wave's last
+    // tile reads are done) and out as whole rows: stored straight from the
+    // accumulators, each instruction wrote 8 bytes of 32 rows, and the
+    // partial lines reached HBM piecemeal (measured at BASELINE config 5:
+    // 290.6 MB written for a 134.2 MB output).
+    static_assert(NW * kStageOutBytes <= Tile::LDS_BYTES, "output staging must fit the tile area");
+    __syncthreads();
+    if (wave_active)
+      stage_rows_store<T, NDB>(acc, inv_l, reinterpret_cast<uint8_t*>(smem) + w * kStageOutBytes,
+                               c32, g, lane,
+                               static_cast<uint16_t*>(p.o) + o_base + (int64_t)wrow0 * p.o_ss,
+                               p.o_ss, Sq - wrow0);
+    if (p.lse != nullptr && g == 0 && row_valid) p.lse[lse_base + (int64_t)qi * p.lse_ss] = lse_val;
+    return;
+  }
   if (!row_valid) return;
 
   uint16_t* orow = static_cast<uint16_t*>(p.o) + o_base + (int64_t)qi * p.o_ss;
