@@ -158,9 +158,12 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
       return launch_prefill_pp<T, D, false>(p, st);
     }
     // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
-    // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves.
+    // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves, in
+    // workgroups of 2 (64 rows; measured at BASELINE config 5: 4 % faster
+    // than 4-wave workgroups, which visit more key tiles per row at a window
+    // edge; 3 waves per SIMD spill and were 3.3x slower, 64-key tiles 1.6x).
     if (masked) {
-      if constexpr (GEN) return launch_prefill_cfg<T, D, 4, 32, GEN, 2>(p, st);
+      if constexpr (GEN) return launch_prefill_cfg<T, D, 2, 32, GEN, 2>(p, st);
       else return launch_prefill_cfg<T, D, 4, 32, GEN, 3>(p, st);
     }
     return launch_prefill_cfg<T, D, 8, 64, GEN, 2>(p, st);
