@@ -282,10 +282,14 @@ void prefill_kernel(const FwdParams p) {
   float l_run = 0.f;         // this lane's partial row sum
 
   // S^T of one tile from a K slot (v_mfma_f32_32x32x16: A = K rows, B = Q^T).
+  // C operand the S^T products start from: zero, or with causal ALiBi on the
+  // fast transform below, the per-slot ALiBi term divided by the score
+  // scale (set there).
+  f32x16 cinit = f32x16{};
   auto qk = [&](const uint16_t* Ks, f32x16* sd) {
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb) {
-      sd[kb] = f32x16{};
+      sd[kb] = cinit;
 #pragma unroll
       for (int kc = 0; kc < NKC; ++kc) {
         const u32x4 a = load16(Ks + (kb * 32 + c32) * KSTR + kc * 16 + g * 8);
@@ -318,9 +322,11 @@ void prefill_kernel(const FwdParams p) {
   // of them under causal masking: the keys past it are masked),
   // -k slope |qpos - key| = A - akk with A = ak (qpos - n0 - 4g - 32 kb) per
   // lane and 32-key block, ak = -k slope, and akk = ak koff per score slot
-  // (koff < 32 the slot's key offset in the block, the same in every lane):
-  // one FMA and one add per score.  (The 8-wave D = 128 tiles have no
-  // registers left for akk and take the |qpos - key| form.)
+  // (koff < 32 the slot's key offset in the block, the same in every lane).
+  // Causal launches start the S^T products from C = -akk / k (cinit), so the
+  // MFMAs add the per-slot term and the transform is one FMA per score;
+  // otherwise one FMA and one more per score.  (The 8-wave D = 128 tiles
+  // take the |qpos - key| form.)
   constexpr bool kFastT = GENERIC && !BIAS && D < 256;
   constexpr bool kAkk = kFastT && (NKB == 1 || D <= 64);
   const bool alibi_on = GENERIC && p.alibi != nullptr;
@@ -329,10 +335,10 @@ void prefill_kernel(const FwdParams p) {
   const float ak = GENERIC ? -slope * (p.softcap > 0.f ? p.softcap_k : kLog2e) : 0.f;
   const float c2 = p.softcap * kLog2e, m2c2 = -2.f * c2;
   auto koff = [](int kb, int v) __attribute__((always_inline)) { return kb * 32 + 8 * (v >> 2) + (v & 3); };
-  float akk[kAkk ? 16 : 1];
-  if constexpr (kAkk) {
+  if (kAkk && alibi_on && causal) {
+    const float akt = -ak / tk;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) akk[v] = ak * (float)koff(0, v);
+    for (int v = 0; v < 16; ++v) cinit[v] = akt * (float)koff(0, v);
   }
 
   // Softmax of one tile of scores starting at key n0: GENERIC transform,
@@ -366,12 +372,20 @@ void prefill_kernel(const FwdParams p) {
     } else if (kFastT) {
       if (alibi_on) {
         const int dq0 = qp32 - n0 - 4 * g;   // qpos - key = dq0 - koff
-        if (kAkk && (causal || n0 + BN - 1 <= qpos_w_min)) {
+        if (kAkk && causal) {
 #pragma unroll
           for (int kb = 0; kb < NKB; ++kb) {
             const float A = ak * (float)(dq0 - 32 * kb);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) sc[kb][v] = fmaf(sc[kb][v], tk, A) - akk[kAkk ? v : 0];
+            for (int v = 0; v < 16; ++v) sc[kb][v] = fmaf(sc[kb][v], tk, A);
+          }
+        } else if (kAkk && n0 + BN - 1 <= qpos_w_min) {
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+            const float A = ak * (float)(dq0 - 32 * kb);
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              sc[kb][v] = fmaf(-ak, (float)koff(0, v), fmaf(sc[kb][v], tk, A));
           }
         } else {
 #pragma unroll
