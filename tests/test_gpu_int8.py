@@ -150,6 +150,61 @@ def test_int8_baseline_c3_sampled(causal):
                      torch.float16)
 
 
+def _int8_torch_reference(q8, s_q, k8, s_k, v, causal, scale):
+    """The INT8-QK semantics in fp32 torch on the GPU for one batch of heads:
+    q8/k8 [H, S, D] int8 values (as float32), s_q/s_k [H, S]; the integer dot
+    products (|sum| <= 128 * 127^2 < 2^24) are exact in fp32."""
+    qk = torch.matmul(q8, k8.transpose(1, 2).contiguous())
+    sc = qk * (s_q[:, :, None] * s_k[:, None, :]) * scale
+    if causal:
+        S = sc.shape[-1]
+        i = torch.arange(S, device=sc.device)
+        sc.masked_fill_(i[None, :] > i[:, None], float("-inf"))
+    return torch.matmul(torch.softmax(sc, dim=-1), v)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_int8_baseline_c3_every_row(causal):
+    # BASELINE config 3 in full, every output row, against the INT8 semantics
+    # in fp32 torch (Q quantized by the oracle's fp32 restatement, K8 / s_k
+    # from the kernel's prepass, which the sampled test above checks byte for
+    # byte); the torch reference is checked against the float64 oracle first.
+    from flash_attn_triton.triton_kernel.attention_kernel_int8 import (attention_int8,
+                                                                      quantize_k_int8)
+    B, H, S, D = 4, 32, 4096, 128
+    scale = 1.0 / math.sqrt(D)
+    q = randn((B, H, S, D), 4)
+    k = randn((B, H, S, D), 5)
+    gen = torch.Generator().manual_seed(6)
+    for b in range(B):
+        for h in range(H):
+            rows = torch.randperm(S, generator=gen)[:41]
+            k[b, h, rows] = (k[b, h, rows].float() * 8.0).half()
+    v = randn((B, H, S, D), 7)
+    kd = k.to(DEV)
+    k8, s_k = quantize_k_int8(kd)
+    out = attention_int8(q.to(DEV), kd, v.to(DEV), causal=causal)
+    q8n, s_qn = quant.quantize_q_rows(q.numpy())
+    q8 = torch.from_numpy(q8n.astype(np.float32)).to(DEV)
+    s_q = torch.from_numpy(s_qn.astype(np.float32)).to(DEV)
+    k8f = k8.to(torch.float32).reshape(B, H, S, D)
+    s_kf = s_k.reshape(B, H, S)
+    # The reference on one head's first 256 rows and keys against the oracle.
+    small = _int8_torch_reference(q8[0, :1, :256], s_q[0, :1, :256], k8f[0, :1, :256],
+                                  s_kf[0, :1, :256], v[0, :1, :256].to(DEV).float(), causal, scale)
+    ora_small, _ = quant.attention_int8(q[0:1, 0:1, :256].numpy(), k[0:1, 0:1, :256].numpy(),
+                                        to_np(v[0:1, 0:1, :256]), causal=causal)
+    assert np.max(np.abs(to_np(small.cpu()) - ora_small[0])) < 1e-5
+    vd = v.to(DEV).float()
+    worst = 0.0
+    for b in range(B):
+        ref = _int8_torch_reference(q8[b], s_q[b], k8f[b], s_kf[b], vd[b], causal, scale)
+        worst = max(worst, float((out[b].float() - ref).abs().max()))
+        assert_close(to_np(out[b].cpu()), to_np(ref.cpu()), INT8_ATOL, f"int8 b={b}", torch.float16)
+        del ref
+    print(f"C3 full causal={causal}: raw max-abs error {worst:.3e}")
+
+
 def _int8_grad_check(name, got, exact):
     # The reference's INT8 gradient bars against unquantized attention
     # (tests/test_compare_implementations.py:27-28, :221-235): the INT8

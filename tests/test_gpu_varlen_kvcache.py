@@ -80,6 +80,64 @@ def test_varlen_baseline_c5_features(dtype):
                  window_right=0, softcap=30.0, alibi=slopes, seed=40, dtype=dtype)
 
 
+def _c5_torch_reference(q, k, v, cu, slopes, left, cap):
+    """fp32 torch attention per sequence on the GPU with the reference's score
+    pipeline (scale, ALiBi -slope |i - j|, softcap tanh, causal + left window
+    mask, softmax, P V); q/k/v [T, H, D] on the device.  Pinned against the
+    float64 oracle in test_varlen_c5_full_every_row."""
+    H, D = q.shape[1], q.shape[2]
+    scale = 1.0 / math.sqrt(D)
+    out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    sl = slopes.float().to(q.device)[:, None, None]
+    for b in range(len(cu) - 1):
+        s, e = int(cu[b]), int(cu[b + 1])
+        L = e - s
+        qs, ks, vs = (t[s:e].float().transpose(0, 1).contiguous() for t in (q, k, v))
+        sc = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * scale
+        i = torch.arange(L, device=q.device)
+        dist = (i[:, None] - i[None, :]).float()
+        sc = sc - sl * dist.abs()
+        sc = cap * torch.tanh(sc / cap)
+        sc.masked_fill_((dist < 0) | (dist > left), float("-inf"))
+        out[s:e] = torch.matmul(torch.softmax(sc, dim=-1), vs).transpose(0, 1)
+        del sc
+    return out
+
+
+def test_varlen_c5_full_every_row():
+    # BASELINE config 5 in full (the bench's workload: 32 sequences U[128, 4096],
+    # generator seed 0), every output row, through the public API, against
+    # an fp32 torch reference on the GPU; the float64 oracle is too slow at
+    # this size, so the reference is first checked against the oracle on two
+    # short sequences with the same features.
+    from flash_attn_triton import flash_attn_varlen_func
+    H, D, left, cap = 16, 128, 1024, 30.0
+    slopes = 2.0 ** (-8.0 * (torch.arange(H) + 1) / H)
+
+    small = [300, 77]
+    cs = _cu(small)
+    qs, ks, vs = (randn((sum(small), H, D), s, torch.float32) for s in (51, 52, 53))
+    ref_small = _c5_torch_reference(qs.to(DEV), ks.to(DEV), vs.to(DEV), cs.tolist(), slopes, left, cap)
+    ora_small, _ = ora.attention_varlen(to_np(qs), to_np(ks), to_np(vs), cs.numpy(), cs.numpy(),
+                                        1.0 / math.sqrt(D), True, (left, 0), cap, to_np(slopes))
+    assert np.max(np.abs(to_np(ref_small.cpu()) - ora_small)) < 1e-5
+
+    gen = torch.Generator().manual_seed(0)
+    lengths = torch.randint(128, 4097, (32,), generator=gen).tolist()
+    cu = _cu(lengths)
+    T = int(cu[-1])
+    q, k, v = (randn((T, H, D), s, torch.float16).to(DEV) for s in (41, 42, 43))
+    out = flash_attn_varlen_func(q, k, v, cu.to(DEV), cu.to(DEV), max(lengths), max(lengths),
+                                 causal=True, window_size=(left, 0), softcap=cap,
+                                 alibi_slopes=slopes.float().to(DEV))
+    ref = _c5_torch_reference(q, k, v, cu.tolist(), slopes, left, cap)
+    torch.cuda.synchronize()
+    raw = float((out.float() - ref).abs().max())
+    print(f"C5 full ({T} tokens x {H} heads, every row): raw max-abs error {raw:.3e}")
+    assert_close(to_np(out.cpu()), to_np(ref.cpu()), ATOL[torch.float16], "C5 full out",
+                 torch.float16)
+
+
 def _paged_setup(lengths, page_size, hk, d, seed, dtype=torch.float16, extra_pages=3):
     pages_per = [(L + page_size - 1) // page_size for L in lengths]
     n_pages = sum(pages_per) + extra_pages
@@ -164,7 +222,8 @@ def test_batched_cache_with_rows_and_leftpad():
 
 
 def test_paged_decode_baseline_c4_sampled():
-    # 64 sequences, L ~ U[512, 8192], page 256, Hq 32, Hk 8, D 128.
+    # 64 sequences, L ~ U[512, 8192], page 256, Hq 32, Hk 8, D 128:
+    # three sequences against the float64 oracle, every sequence against fp32 torch.
     from flash_attn_triton import flash_attn_with_kvcache
     gen = torch.Generator().manual_seed(0)
     lengths = torch.randint(512, 8193, (64,), generator=gen)
@@ -189,3 +248,27 @@ def test_paged_decode_baseline_c4_sampled():
                                              block_table=bt[b:b + 1].numpy(), causal=False)
         assert_close(to_np(out[b:b + 1]), ref, ATOL[torch.float16], f"decode b={b}",
                      torch.float16)
+    # Every sequence against an fp32 torch reference on the GPU (block-table
+    # gather, GQA expansion, softmax, P V), itself checked against the oracle's
+    # result for sequence 0 above.
+    kd, vd, btd = kc.to(DEV).float(), vc.to(DEV).float(), bt.to(DEV).long()
+    qd = q.to(DEV).float()
+    worst = 0.0
+    for b in range(64):
+        L = int(lengths[b])
+        pages = btd[b, :(L + page - 1) // page]
+        kb = kd[pages].reshape(-1, hk, d)[:L].repeat_interleave(hq // hk, dim=1)   # [L, hq, d]
+        vb = vd[pages].reshape(-1, hk, d)[:L].repeat_interleave(hq // hk, dim=1)
+        kt = kb.permute(1, 0, 2).contiguous()                                      # [hq, L, d]
+        vt = vb.permute(1, 0, 2).contiguous()
+        sc = torch.matmul(kt, qd[b, 0][:, :, None])[:, :, 0] / math.sqrt(d)        # [hq, L]
+        ref_b = torch.matmul(torch.softmax(sc, dim=-1)[:, None, :], vt)[:, 0, :]   # [hq, d]
+        if b == 0:
+            ref0, _, _, _ = ora.attention_kvcache(to_np(q[0:1]), to_np(kc), to_np(vc),
+                                                  cache_seqlens=[L], block_table=bt[0:1].numpy(),
+                                                  causal=False)
+            assert np.max(np.abs(to_np(ref_b.cpu()) - ref0[0, 0])) < 1e-5
+        worst = max(worst, float((out[b, 0].to(DEV).float() - ref_b).abs().max()))
+        assert_close(to_np(out[b, 0]), to_np(ref_b.cpu()), ATOL[torch.float16],
+                     f"decode b={b} (fp32 reference)", torch.float16)
+    print(f"C4 full (64 sequences): raw max-abs error {worst:.3e}")
