@@ -31,6 +31,24 @@ inline hipError_t set_lds_limit(std::atomic<uint64_t>& devices, Kern kern, int b
   return e;
 }
 
+// Compute units of the current device (cached per device).
+inline hipError_t device_cus(int* n) {
+  static std::atomic<int> cus[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev >= 0 && dev < 64) {
+    const int c = cus[dev].load(std::memory_order_relaxed);
+    if (c > 0) {
+      *n = c;
+      return hipSuccess;
+    }
+  }
+  e = hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess && dev >= 0 && dev < 64) cus[dev].store(*n, std::memory_order_relaxed);
+  return e;
+}
+
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));

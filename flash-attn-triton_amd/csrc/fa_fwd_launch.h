@@ -35,7 +35,8 @@ hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipS
 
 // Prefill tile table (fa_prefill_kernel.h), keyed by head dim and by whether
 // the problem is masked (causal, window or varlen):
-//   D = 128, masked  : 4 waves, 32-key tiles, 3 waves per SIMD (165 VGPRs)
+//   D = 128, masked  : 4 waves, 32-key tiles, 3 waves per SIMD (165 VGPRs);
+//                      with the generic epilogue 2 waves, 2 per SIMD
 //   D = 128, unmasked: 8 waves (256 query rows share each K/V tile), 64-key tiles
 //   D = 256          : 8 waves, 32-key tiles (the O^T accumulators take 128 VGPRs)
 //   D = 32 / 64      : 4 waves, 64-key tiles
@@ -71,24 +72,6 @@ hipError_t launch_prefill_pp(FwdParams p, hipStream_t st) {
   p.total_blocks = (int)total;
   hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
   return hipGetLastError();
-}
-
-// Compute units of the current device (cached per device).
-inline hipError_t device_cus(int* n) {
-  static std::atomic<int> cus[64];
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  if (dev >= 0 && dev < 64) {
-    const int c = cus[dev].load(std::memory_order_relaxed);
-    if (c > 0) {
-      *n = c;
-      return hipSuccess;
-    }
-  }
-  e = hipDeviceGetAttribute(n, hipDeviceAttributeMultiprocessorCount, dev);
-  if (e == hipSuccess && dev >= 0 && dev < 64) cus[dev].store(*n, std::memory_order_relaxed);
-  return e;
 }
 
 // Persistent ping-pong prefill (fa_prefill_persist.h) when the launch is a

@@ -62,6 +62,7 @@ struct Int8Params {
   float scale_log2;
   int causal, seq_len_k, seq_len_q;
   int n_mblocks, total_blocks;
+  int persist_rounds;   // int8_persist_kernel: row blocks per workgroup
 };
 
 }  // namespace fa

@@ -14,6 +14,7 @@
 // The attention kernel follows the schedule of prefill_kernel
 // (fa_prefill_kernel.h); see int8_fwd_kernel below.
 #include "fa_int8_pp.h"
+#include "fa_int8_persist.h"
 
 namespace fa {
 
@@ -481,12 +482,57 @@ hipError_t launch_int8_pp(Int8Params p, hipStream_t st) {
   return hipGetLastError();
 }
 
-// Tile table: D = 128 -> the ping-pong kernel.  Otherwise causal -> 4 waves,
+// Persistent INT8 kernel (fa_int8_persist.h) for the large dense launches it
+// covers, with the conditions of prefill_persist_kernel's launch: equal
+// query and key lengths in full 256-row blocks (causal: an even number of
+// them, paired), (batch, head) groups a multiple of the 8 XCDs, and a work
+// list that splits evenly over at least 3/4 of the CUs with at least two row
+// blocks per workgroup.  *launched is false (nothing launched) otherwise.
+template <int D>
+hipError_t launch_int8_persist(Int8Params p, hipStream_t st, bool* launched) {
+  using Tile = Int8PersistTile<D>;
+  *launched = false;
+  const bool causal = p.causal != 0;
+  const int64_t S = p.seqlen;
+  const int64_t G = (int64_t)p.batch * p.heads;
+  if (D != 128 || S <= 0 || p.seq_len_k != S || p.seq_len_q != S ||
+      S % (causal ? 2 * Tile::BM : Tile::BM) != 0 || G % 8 != 0 || G > (1 << 24))
+    return hipSuccess;
+  int cus = 0;
+  hipError_t e = device_cus(&cus);
+  if (e != hipSuccess) return e;
+  const int64_t n_mb = S / Tile::BM;
+  const int64_t units = G / 8 * (causal ? n_mb / 2 : n_mb);   // per XCD
+  const int64_t max_slots = cus / 8;
+  int64_t slots = 0;
+  for (int64_t d = max_slots; d >= 1; --d)
+    if (units % d == 0) {
+      slots = d;
+      break;
+    }
+  const int64_t rounds = units / slots * (causal ? 2 : 1);
+  if (slots * 4 < max_slots * 3 || rounds < 2 || n_mb > (1 << 20)) return hipSuccess;
+  p.n_mblocks = (int)n_mb;
+  p.persist_rounds = (int)rounds;
+  auto kern = causal ? int8_persist_kernel<D, true> : int8_persist_kernel<D, false>;
+  static std::atomic<uint64_t> lds_devices_c{0}, lds_devices_n{0};
+  e = set_lds_limit(causal ? lds_devices_c : lds_devices_n, kern, Tile::LDS_BYTES);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(8 * slots)), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  *launched = true;
+  return hipGetLastError();
+}
+
+// Tile table: D = 128 -> the persistent kernel where it applies, else the
+// ping-pong kernel.  Otherwise causal -> 4 waves,
 // 32-key tiles (less work past the diagonal), non-causal 8 waves sharing
 // 64-key tiles; D = 256: 8 waves, 32-key tiles.
 template <int D>
 hipError_t launch_int8_fwd(const Int8Params& p, hipStream_t st) {
   if constexpr (D == 128) {
+    bool launched = false;
+    hipError_t e = launch_int8_persist<D>(p, st, &launched);
+    if (e != hipSuccess || launched) return e;
     return launch_int8_pp<D>(p, st);
   } else if constexpr (D == 256) {
     return launch_int8_cfg<D, 8, 32, 2>(p, st);
