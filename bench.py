@@ -371,8 +371,8 @@ KERNELS = {
     "dense": ("fa::prefill_persist_kernel",),
     "bwd_causal": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
     "bwd": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
-    "int8_causal": ("fa::int8_pp_kernel",),
-    "int8": ("fa::int8_pp_kernel",),
+    "int8_causal": ("fa::int8_persist_kernel",),
+    "int8": ("fa::int8_persist_kernel",),
     "decode": ("fa::decode_kernel", "fa::decode_combine_kernel"),
     "varlen": ("fa::prefill_kernel",),
     "copy": ("__amd_rocclr_copyBuffer",),
