@@ -18,11 +18,12 @@ defect or a host-side copy, never changes a correct result):
   Python loop of gathers and O(L^2) padded launches, and its causal
   alignment is bottom-right for every cache length (the reference's dense
   stage split drops keys past the first tile when ``L > BLOCK_M``);
-* gradients run on HIP backward kernels for fp16 / bf16 dense, cross and
-  varlen calls (deterministic: grouped KV heads are reduced in the kernel,
-  not with atomics); fp32 inputs, ``attn_bias``, seqused / paged varlen and
-  the KV-cache path are forward only (``backward`` raises
-  ``NotImplementedError``);
+* gradients run on HIP backward kernels (deterministic: grouped KV heads
+  are reduced in the kernel, not with atomics) for dense, cross and varlen
+  calls in fp16 / bf16 / fp32, ``attn_bias``, seqused / paged varlen and
+  the KV-cache path, which, when gradients are needed, gathers each
+  sequence's keys as the reference does and runs the dense kernels; fp32 at
+  head dim 256 is forward only (``backward`` raises ``NotImplementedError``);
 * dropout draws its mask from a counter-based Philox4x32-10 generator keyed
   by a seed from torch's default CPU generator, one independent mask per
   (batch, head) (the reference's ``tl.rand`` offsets repeat the same mask for
@@ -486,6 +487,12 @@ def flash_attn_with_kvcache(
         _native.kvcache_append(kn, vn, k_cache, v_cache, lengths32, bt32, rows32, pads32,
                                int(cache_capacity), cos_t, sin_t, rotary_interleaved)
         lengths32 = (lengths32 + n_new).to(torch.int32)
+    if _needs_grad(q, k_cache, v_cache):
+        if launch_first:
+            chk.flush()
+        return _kvcache_differentiable(q, k_cache, v_cache, lengths32, bt32, cache_rows, pads32,
+                                       cos_t, sin_t, rotary_interleaved, softmax_scale, causal,
+                                       window_size, alibi)
     qk = _kernel_ready(q)
     if cos_t is not None and q.shape[1]:
         q_rot = torch.empty(q.shape, dtype=q.dtype, device=q.device)
@@ -505,6 +512,65 @@ def flash_attn_with_kvcache(
     else:
         launch()
     return _wrap_grad(out, q)
+
+
+def _rotary_torch(x, cos_t, sin_t, positions, interleaved):
+    """The query rotation of the KV-cache path (``_native.rotary_q``) as torch
+    ops, differentiable in ``x`` [1, S, H, D]: tables already rounded to the
+    input dtype and held in fp32, the rotation in fp32, one rounding back
+    (reference ``_apply_rotary``, flash_attn_interface.py:52-66)."""
+    half = cos_t.shape[-1]
+    c = cos_t[positions][None, :, None, :]
+    s = sin_t[positions][None, :, None, :]
+    xf = x.float()
+    xr, rest = xf[..., :2 * half], xf[..., 2 * half:]
+    if interleaved:
+        x1, x2 = xr[..., 0::2], xr[..., 1::2]
+        rot = torch.stack((x1 * c - x2 * s, x1 * s + x2 * c), dim=-1).flatten(-2)
+    else:
+        x1, x2 = xr[..., :half], xr[..., half:]
+        rot = torch.cat((x1 * c - x2 * s, x1 * s + x2 * c), dim=-1)
+    return torch.cat((rot, rest), dim=-1).to(x.dtype)
+
+
+def _kvcache_differentiable(q, k_cache, v_cache, lengths32, bt32, cache_rows, pads32, cos_t,
+                            sin_t, interleaved, softmax_scale, causal, window_size, alibi):
+    """The KV-cache attention when gradients are needed, as the reference
+    computes it (flash_attn_interface.py:494-525): per sequence, its keys
+    gathered from the cache by differentiable indexing and the dense
+    attention with query row i at position i + L - Sq (causal) on the HIP
+    forward / backward kernels.  Gradients reach q, k_cache and v_cache (the
+    rows a sequence reads); the new k / v of an append are written into the
+    cache beforehand and get none, as in the reference, whose append writes
+    into a copy."""
+    batch, sq = q.shape[0], q.shape[1]
+    hk, d = k_cache.shape[2], k_cache.shape[3]
+    lens = lengths32.tolist()
+    pads = pads32.tolist() if pads32 is not None else [0] * batch
+    rows = cache_rows.tolist() if cache_rows is not None else list(range(batch))
+    outs = []
+    for b in range(batch):
+        L, st = int(lens[b]), int(pads[b])
+        qb = q[b:b + 1]
+        if cos_t is not None and sq:
+            pos = torch.arange(sq, device=q.device) + (L - sq + st)
+            qb = _rotary_torch(qb, cos_t, sin_t, pos, interleaved)
+        if L == 0 or sq == 0:
+            outs.append(torch.zeros(qb.shape, dtype=q.dtype, device=q.device))
+            continue
+        if bt32 is not None:
+            page = k_cache.shape[1]
+            pages = bt32[b, :(st + L + page - 1) // page].long()
+            kb = k_cache[pages].reshape(-1, hk, d)[st:st + L]
+            vb = v_cache[pages].reshape(-1, hk, d)[st:st + L]
+        else:
+            kb = k_cache[rows[b], st:st + L]
+            vb = v_cache[rows[b], st:st + L]
+        outs.append(dense_attention(
+            qb, kb.unsqueeze(0), vb.unsqueeze(0), softmax_scale=softmax_scale, causal=causal,
+            q_pos_offset=(L - sq) if causal else 0, window_left=window_size[0],
+            window_right=window_size[1], alibi=None if alibi is None else alibi[b:b + 1]))
+    return torch.cat(outs, dim=0)
 
 
 def _packed_index(starts, lengths, device):

@@ -207,6 +207,95 @@ def test_baseline_c2_sampled_heads():
             _check(f"{name}[{b},{h}]", t.grad[sl], r, torch.float16)
 
 
+def _kvcache_grad_case(paged, causal, rotary=False, alibi=False, window=(-1, -1), seed=300):
+    # Gradients through flash_attn_with_kvcache against the float64 oracle
+    # run per sequence on the gathered keys (the reference's own
+    # computation, flash_attn_interface.py:494-525), the key gradients
+    # scattered back into the cache's rows.
+    from flash_attn_triton import flash_attn_with_kvcache
+    B, Sq, Hq, Hk, D = 3, 4, 4, 2, 64
+    lengths = [70, 131, 9]
+    if paged:
+        page = 64
+        pages_per = [(L + page - 1) // page for L in lengths]
+        n_pages = sum(pages_per) + 2
+        perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed))
+        bt = torch.zeros((B, max(pages_per)), dtype=torch.int32)
+        pos = 0
+        for b, n in enumerate(pages_per):
+            bt[b, :n] = perm[pos:pos + n].to(torch.int32)
+            pos += n
+        kc = randn((n_pages, page, Hk, D), seed + 1)
+        vc = randn((n_pages, page, Hk, D), seed + 2)
+        rows, pads = None, [0] * B
+    else:
+        cap = 160
+        kc = randn((B + 1, cap, Hk, D), seed + 1)
+        vc = randn((B + 1, cap, Hk, D), seed + 2)
+        rows, pads, bt = [2, 0, 3], [5, 0, 17], None
+    q = randn((B, Sq, Hq, D), seed + 3)
+    do = randn((B, Sq, Hq, D), seed + 4)
+    slopes = (torch.rand(Hq, generator=torch.Generator().manual_seed(seed + 5)) * 0.3
+              if alibi else None)
+    cos = sin = None
+    if rotary:
+        ang = torch.arange(256, dtype=torch.float32)[:, None] * (
+            1e-2 * torch.arange(1, D // 4 + 1, dtype=torch.float32))[None, :]
+        cos, sin = torch.cos(ang), torch.sin(ang)
+    qd, kcd, vcd = (t.to(DEV).requires_grad_() for t in (q, kc, vc))
+    out = flash_attn_with_kvcache(
+        qd, kcd, vcd, cache_seqlens=torch.tensor(lengths, dtype=torch.int32).to(DEV),
+        block_table=None if bt is None else bt.to(DEV),
+        cache_batch_idx=None if rows is None else torch.tensor(rows, dtype=torch.int32).to(DEV),
+        cache_leftpad=None if paged else torch.tensor(pads, dtype=torch.int32).to(DEV),
+        rotary_cos=None if cos is None else cos.to(DEV), rotary_sin=None if sin is None else sin.to(DEV),
+        rotary_interleaved=False, causal=causal, window_size=window,
+        alibi_slopes=None if slopes is None else slopes.to(DEV))
+    out.backward(do.to(DEV))
+    torch.cuda.synchronize()
+    scale = 1.0 / math.sqrt(D)
+    dq_ref = np.zeros(q.shape)
+    dk_ref, dv_ref = np.zeros(kc.shape), np.zeros(vc.shape)
+    cos_h = None if cos is None else cos.half().double().numpy()
+    sin_h = None if sin is None else sin.half().double().numpy()
+    for b, L in enumerate(lengths):
+        st = pads[b]
+        if paged:
+            page = kc.shape[1]
+            j = np.arange(L)
+            idx = (bt[b].numpy()[j // page].astype(np.int64), j % page)
+        else:
+            idx = (np.full(L, rows[b]), st + np.arange(L))
+        kb, vb = to_np(kc)[idx][None], to_np(vc)[idx][None]
+        qb = to_np(q[b:b + 1])
+        pos = np.arange(Sq) + L - Sq + st
+        if rotary:
+            qb = ora.apply_rotary(qb, cos_h, sin_h, pos, False)
+        dqb, dkb, dvb = ora.attention_backward(
+            qb, kb, vb, to_np(do[b:b + 1]), scale, causal, window, 0.0,
+            None if slopes is None else slopes.double().numpy(),
+            causal_offset=(L - Sq) if causal else 0)
+        if rotary:   # the rotation is orthogonal: back through it with the angle negated
+            dqb = ora.apply_rotary(dqb, cos_h, -sin_h, pos, False)
+        dq_ref[b] = dqb[0]
+        np.add.at(dk_ref, idx, dkb[0])
+        np.add.at(dv_ref, idx, dvb[0])
+    _check("dq", qd.grad, dq_ref, torch.float16)
+    _check("dk_cache", kcd.grad, dk_ref, torch.float16)
+    _check("dv_cache", vcd.grad, dv_ref, torch.float16)
+
+
+@pytest.mark.parametrize("paged", [True, False])
+@pytest.mark.parametrize("causal", [False, True])
+def test_kvcache_gradients(paged, causal):
+    _kvcache_grad_case(paged, causal)
+
+
+def test_kvcache_gradients_rotary_alibi_window():
+    _kvcache_grad_case(True, True, rotary=True, alibi=True, window=(40, 0), seed=320)
+    _kvcache_grad_case(False, False, rotary=True, window=(16, 8), seed=340)
+
+
 def test_forward_only_paths_raise_on_backward():
     # fp32 at head dim 256 has no backward (its K^T / V^T registers would not fit).
     from flash_attn_triton import flash_attn_func
