@@ -91,3 +91,10 @@ def test_persistent_baseline_config_c2_every_row(causal):
     # BASELINE config 2 at full size (B=4, H=32, S=4096, D=128): eight row
     # blocks per workgroup, every output row and LSE checked.
     _case(4, 4096, 32, 32, causal, seed=40)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_persistent_long_sequence(causal):
+    # S = 8192: 32 row blocks per (batch, head) group, 16 groups, two rounds
+    # per workgroup; causal pairs span 8192 keys.
+    _case(1, 8192, 16, 16, causal, seed=50)
