@@ -90,12 +90,14 @@ bool needs_generic(const fa::FwdParams& p) {
 // fa_common.h); p = 0 disables it.  An element is kept with probability
 // (65536 - t16) / 65536, so kept values are scaled by the reciprocal of that,
 // which makes the mask unbiased for the 16-bit threshold (1 / (1 - p) up to
-// 2^-17 / (1 - p)).  A p that rounds to t16 = 65536 would keep nothing and is
-// rejected, as is p outside [0, 1).
+// 2^-17 / (1 - p)).  Every p in [0, 1) is accepted, as the reference does
+// (flash_attn_interface.py:99): a p within 2^-17 of 1 would round to
+// t16 = 65536 and keep nothing, so t16 stops at 65535 (one element in 65536
+// kept, scaled by 65536).  p outside [0, 1) is rejected.
 bool fill_dropout(fa::DropoutCfg& d, float p, uint64_t seed) {
   if (!(p >= 0.f && p < 1.f)) return false;
   d.t16 = (int)nearbyint((double)p * 65536.0);
-  if (d.t16 >= 65536) return false;
+  if (d.t16 > 65535) d.t16 = 65535;
   d.enabled = d.t16 > 0;
   d.seed_lo = (uint32_t)(seed & 0xffffffffu);
   d.seed_hi = (uint32_t)(seed >> 32);
@@ -525,15 +527,17 @@ int fa_kvcache_run(const char* name, const void* q, const void* k_cache, const v
   if (num_splits != plan.num_splits)
     return fail(FA_ERR_INVALID, "%s: num_splits %d does not match the plan (%d)", name,
                 (int)num_splits, plan.num_splits);
-  if (plan.num_splits > 1 &&
+  // Nothing to compute: no launch, and no workspace is read.
+  if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
+  // fp32 runs every key of a row in one workgroup: the plan's split count is
+  // checked above (the contract is dtype-independent) but no split is used,
+  // so the workspace is neither needed nor read.
+  const bool f32 = dtype == FA_DTYPE_F32;
+  if (plan.num_splits > 1 && !f32 &&
       (!workspace || workspace_bytes < plan.o_part_bytes + plan.lse_part_bytes ||
        reinterpret_cast<uintptr_t>(workspace) % 16 != 0))
     return fail(FA_ERR_INVALID, "%s: workspace too small or misaligned (%lld < %lld)", name,
                 (long long)workspace_bytes, (long long)(plan.o_part_bytes + plan.lse_part_bytes));
-  if (batch == 0 || seqlen_q == 0) return hip_status(hipSuccess, "");
-  // fp32 runs every key of a row in one workgroup: the plan's split count is
-  // checked above (the contract is dtype-independent) but no split is used.
-  const bool f32 = dtype == FA_DTYPE_F32;
   if (plan.decode && !f32) {
     fa::DecodeParams d{};
     d.q = q; d.k = k_cache; d.v = v_cache; d.o = out; d.lse = lse;

@@ -71,6 +71,9 @@ extern "C" int fa_fwd_kvcache_noalloc(
   int st = fa_fwd_kvcache_plan(batch, seqlen_q, heads_q, heads_k, head_dim, max_keys,
                                block_table ? page_size : 0, &splits, &need);
   if (st != FA_OK) return st;
+  // fp32 never splits the keys of a row (no workspace is read), and an empty
+  // call launches nothing: neither needs the scratch array.
+  if (dtype == FA_DTYPE_F32 || batch == 0 || seqlen_q == 0) need = 0;
   if (need > kScratchBytes) {
     char msg[200];
     snprintf(msg, sizeof(msg),
@@ -80,7 +83,7 @@ extern "C" int fa_fwd_kvcache_noalloc(
     return fa_set_error(FA_ERR_UNSUPPORTED, msg);
   }
   void* ws = nullptr;
-  if (need > 0 && batch > 0 && seqlen_q > 0) {
+  if (need > 0) {
     st = scratch_on_current_device(&ws);
     if (st != FA_OK) return st;
   }

@@ -450,7 +450,7 @@ def flash_attn_with_kvcache(
             chk.check_range(lengths, 0, cache_capacity, bad_lengths)
         else:
             chk.check_range(lengths, 0, None, bad_lengths)
-            chk.check_range(lengths.long() + leftpads, None, cache_capacity, bad_lengths)
+            chk.check_range(lengths, None, cache_capacity, bad_lengths, plus=leftpads)
     if cos_t is not None and lengths.numel() and q.shape[1]:
         # Query rows rotate at L + leftpad - Sq + i (L after the append);
         # negative positions index from the end of the tables, as torch

@@ -64,12 +64,12 @@ const char* fa_last_error_string(void);
  * natural-log logsumexp at lse[b*lse_stride[0] + h*lse_stride[1] +
  * i*lse_stride[2]]; rows with no visible key get out = 0 and lse = -inf.
  *
- * dropout_p in [0, 1 - 2^-17] drops probabilities before the product with V
+ * dropout_p in [0, 1) drops probabilities before the product with V
  * (attention_kernel.py:344-358): element (b, h, i, j) is kept iff its 16-bit
- * Philox4x32-10 draw under dropout_seed is >= t16 = round(p * 65536), and kept
- * values are scaled by 65536 / (65536 - t16), the reciprocal of the keep
- * probability (1 / (1 - p) to within 2^-17 / (1 - p)), so the mask is
- * unbiased; p < 2^-17 keeps everything.  The LSE is that of the undropped
+ * Philox4x32-10 draw under dropout_seed is >= t16 = min(round(p * 65536),
+ * 65535), and kept values are scaled by 65536 / (65536 - t16), the
+ * reciprocal of the keep probability (1 / (1 - p) to within 2^-17 / (1 - p)
+ * below p = 1 - 2^-17), so the mask is unbiased; p < 2^-17 keeps everything.  The LSE is that of the undropped
  * scores.
  * The draw of (b, h, i, j) is half j%4 + 4((j%16)/8) of the Philox call with
  * counter {2(j/16) + (j/4)%2, i, h, b} and key {seed, seed >> 32}; rows and
@@ -326,6 +326,23 @@ int fa_rotary_q(const void* q, void* out, const int32_t* cache_seqlens,
                 int64_t rotary_dim, int64_t rotary_rows, int rotary_interleaved, int64_t batch,
                 int64_t seqlen_q, int64_t heads, int64_t head_dim, const int64_t* q_stride,
                 const int64_t* out_stride, int dtype, fa_stream_t stream);
+
+/* Range checks of integer device arrays in one launch: the validation of the
+ * KV-cache call's device arguments (replaces the `torch.any(...)` / `.item()`
+ * chain of flash_attn_interface.py:428-453 that checks the block table,
+ * cache_seqlens, cache_batch_idx and cache_leftpad, one host synchronization
+ * each).  For i < n (1 <= n <= FA_MAX_RANGE_CHECKS): array a[i] holds numel[i]
+ * integers of a_bytes[i] (4 or 8) bytes; b[i] (b or b[i] may be NULL) an
+ * addend of the same length and b_bytes[i] bytes; minmax[2i] and minmax[2i+1]
+ * receive min and max of a[i][j] + b[i][j] over j as int64 (INT64_MAX and
+ * INT64_MIN for an empty array).  minmax is device memory or pinned host
+ * memory (checked with hipPointerGetAttributes; anything else is rejected),
+ * so a host that passes pinned memory reads the results after an event on the
+ * stream, with no copy.  a/b are device arrays.  One workgroup per array. */
+#define FA_MAX_RANGE_CHECKS 8
+int fa_check_ranges(int n, const void* const* a, const int* a_bytes, const void* const* b,
+                    const int* b_bytes, const int64_t* numel, int64_t* minmax,
+                    fa_stream_t stream);
 
 /* Per-token INT8 quantization of K (fp16), bit-exact with
  * `_quantize_k_rows` (attention_kernel_int8.py:58-79, launched at :232):

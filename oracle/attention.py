@@ -83,7 +83,8 @@ def dropout_factors(seed: int, p: float, batch_ids, heads: int, q_len: int,
     ``t16 = round(p * 65536)``: the reciprocal of the keep probability the
     16-bit draws actually give, so the mask is unbiased (equal to the
     reference's ``1 / (1 - p)`` when ``p * 65536`` is an integer).  A ``p`` that
-    rounds to ``t16 = 65536`` (no element kept) is rejected, as the C ABI does.
+    would round to ``t16 = 65536`` (no element kept) takes ``t16 = 65535``, as
+    the C ABI does, so every ``p`` in [0, 1) is accepted (flash_attn_interface.py:99).
 
     Element (b, h, i, j) keeps iff its 16-bit draw >= round(p * 65536).  Its
     draw is half ``e = j % 4 + 4 ((j % 16) // 8)`` (word e // 2, high half
@@ -94,9 +95,7 @@ def dropout_factors(seed: int, p: float, batch_ids, heads: int, q_len: int,
     with every head drawing its own mask.
     """
     p32 = float(np.float32(p))          # the C ABI takes p as an fp32 value
-    t16 = max(0, int(round(p32 * 65536.0)))
-    if t16 >= 65536:
-        raise ValueError("dropout_p rounds to a keep probability of 0 at 16-bit draws")
+    t16 = min(65535, max(0, int(round(p32 * 65536.0))))
     scale = 65536.0 / (65536.0 - t16)
     b = np.asarray(batch_ids, dtype=np.int64)[:, None, None, None]
     h = np.arange(heads, dtype=np.int64)[None, :, None, None]

@@ -179,3 +179,56 @@ def test_noalloc_rejects_workspace_beyond_scratch_without_a_device(lib):
     status = lib.fa_fwd_kvcache_noalloc(*args)
     assert status == _native.FA_ERR_UNSUPPORTED
     assert b"scratch" in lib.fa_last_error_string()
+
+
+def _integration_snippet():
+    """The reference-side binding that INTEGRATION.md shows a maintainer (the
+    first Python block that loads the library), executed with its ``CDLL``
+    pointed at this build's library (a fresh handle, so the snippet's argtypes
+    do not touch the package's own binding)."""
+    text = (Path(__file__).resolve().parents[1] / "INTEGRATION.md").read_text()
+    blocks = re.findall(r"```python\n(.*?)```", text, flags=re.S)
+    code = next(b for b in blocks if "ctypes.CDLL" in b)
+    real_cdll = ctypes.CDLL
+    ns = {}
+    try:
+        ctypes.CDLL = lambda name, *a, **kw: real_cdll(str(_native.library_path()), *a, **kw)
+        exec(compile(code, "INTEGRATION.md", "exec"), ns)
+    finally:
+        ctypes.CDLL = real_cdll
+    return ns
+
+
+def test_integration_binding_matches_header_and_dtype_codes():
+    """The documented ctypes stub passes fa_fwd_dense's arguments with the
+    header's arity and the package's argument types, and maps dtypes to the
+    header's FA_DTYPE_* codes: fp16 -> FA_DTYPE_F16, fp32 -> FA_DTYPE_F32;
+    anything the reference rejects (flash_attn_interface.py:95-96) raises."""
+    ns = _integration_snippet()
+    args = ns["_lib"].fa_fwd_dense.argtypes
+    assert len(args) == _declarations()["fa_fwd_dense"]
+    assert list(args) == list(_native._SIGNATURES["fa_fwd_dense"][1])
+    codes = dict(re.findall(r"#define (FA_DTYPE_\w+) (\d+)", HEADER.read_text()))
+    assert ns["_dtype_code"](torch.float16) == int(codes["FA_DTYPE_F16"]) \
+        == _native.dtype_code(torch.float16)
+    assert ns["_dtype_code"](torch.float32) == int(codes["FA_DTYPE_F32"]) \
+        == _native.dtype_code(torch.float32)
+    for bad in (torch.bfloat16, torch.float64, torch.int32):
+        with pytest.raises(ValueError):
+            ns["_dtype_code"](bad)
+
+
+def test_kvcache_empty_batch_needs_no_workspace(lib):
+    # batch == 0 launches nothing, so the NULL workspace the header allows
+    # for a size-0 plan is accepted even where the plan would split; the
+    # no-allocation variant returns before touching its scratch array.
+    st = _native._strides((4096, 4096, 128))
+    one = ctypes.c_void_p(16)   # never dereferenced: nothing is launched
+    head = (one, one, one, one, None, one, one, 32, 256, 64, None, None)
+    tail = (st, st, st, st, None, _native.FA_DTYPE_F16, 0.088, 0, -1, -1, None, 0)
+    splits, _ = _native.kvcache_plan(0, 1, 32, 8, 128, 8192, 256)
+    assert lib.fa_fwd_kvcache(*head, 0, 1, 8192, 32, 8, 128, *tail, splits, None, 0,
+                              None) == _native.FA_OK
+    assert lib.fa_fwd_kvcache_noalloc(*head, 0, 1, 8192, 32, 8, 128, *tail,
+                                      None) == _native.FA_OK
+

@@ -418,13 +418,15 @@ def test_dropout_keep_rate_and_scale(p):
     assert abs(agree - (p * p + (1 - p) ** 2)) < 0.01
 
 
-@pytest.mark.parametrize("p", [1e-7, 2.0 ** -17, 3e-5, 0.25, 1 - 2.0 ** -12, 1 - 2.0 ** -16])
+@pytest.mark.parametrize("p", [1e-7, 2.0 ** -17, 3e-5, 0.25, 1 - 2.0 ** -12, 1 - 2.0 ** -16,
+                               1 - 2.0 ** -18])
 def test_dropout_mask_is_unbiased(p):
     # E[factor] = keep probability x kept scale must be exactly 1 for every
     # p the 16-bit draws can express, including the extremes: p below
     # 2^-17 keeps everything at scale 1, p = 1 - 2^-16 keeps one draw value
-    # in 65536 at scale 65536.
-    t16 = round(float(np.float32(p)) * 65536)
+    # in 65536 at scale 65536, and so does p = 1 - 2^-18, whose threshold
+    # would round to 65536 (nothing kept) and stops at 65535.
+    t16 = min(65535, round(float(np.float32(p)) * 65536))
     f = ora.dropout_factors(99, p, [0, 1, 2, 3], 8, 128, 256)
     kept = f > 0
     if t16 == 0:
@@ -439,9 +441,13 @@ def test_dropout_mask_is_unbiased(p):
     assert abs(kept.mean() - q_keep) <= 6 * math.sqrt(q_keep * (1 - q_keep) / n) + 1.0 / n
 
 
-def test_dropout_rejects_p_that_keeps_nothing():
-    with pytest.raises(ValueError):
-        ora.dropout_factors(1, 1 - 2.0 ** -18, [0], 1, 4, 4)
+def test_dropout_p_near_one_keeps_one_draw_value():
+    # p = 1 - 2^-18 would round to t16 = 65536 (nothing kept); the threshold
+    # stops at 65535, the threshold of p = 1 - 2^-16, so both give one mask.
+    a = ora.dropout_factors(1, 1 - 2.0 ** -18, [0, 1], 4, 256, 256)
+    b = ora.dropout_factors(1, 1 - 2.0 ** -16, [0, 1], 4, 256, 256)
+    np.testing.assert_array_equal(a, b)
+    assert set(np.unique(a)) <= {0.0, 65536.0}
 
 
 def test_dropout_mask_is_seed_dependent_and_p0_is_identity():
