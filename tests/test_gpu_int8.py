@@ -203,6 +203,7 @@ def _int8_every_row(B, H, S, causal, seed, label):
         assert_close(to_np(out[b].cpu()), to_np(ref.cpu()), INT8_ATOL, f"int8 b={b}", torch.float16)
         del ref
     print(f"{label} causal={causal}: raw max-abs error {worst:.3e}")
+    assert worst <= INT8_ATOL, f"{label}: raw max-abs error {worst:.3e} > 2e-2"
 
 
 @pytest.mark.parametrize("causal", [True, False])
