@@ -18,14 +18,18 @@ is measured in algorithmic bytes (K/V rows read + q + out + block table).
 
 Before the W warmup steps every measurement runs untimed steps for
 ``--prewarm`` seconds (default 0.5) so that the timed steps see settled GPU
-clocks; the line reports how many (``prewarm_steps``).  The timed region is
-exactly K steps either way.
+clocks; the line reports how many (``prewarm_steps``).  The timed region of
+the whole-job value is exactly K steps, with nothing else between its two
+synchronizations.
 
 The JSON line carries ``roofline`` and ``cpu_baseline``.  ``roofline.achieved``
 is the algorithmic work of one launch divided by the mean duration of the
 C-ABI launch of the dominant kernel (HIP events recorded on the launch stream
-around every such call inside the timed region; for decode the split and
-combine kernels together), against the MI355X published peak.
+around every such call in a second timed run of the same K steps; for decode
+the split and combine kernels together), against the MI355X published peak.
+The events are a run of their own because they are packets on the stream
+between the launches and slow the whole job down (by about 13 us per 200 us
+decode step).
 ``roofline.traffic`` is HBM bytes per launch from two ``rocprofv3 --pmc`` child
 runs (FETCH_SIZE, WRITE_SIZE), each scaled by what the same counter reads for
 a 1 GiB device copy; ``--traffic off`` skips them.  ``cpu_baseline`` is the
@@ -46,6 +50,7 @@ its whole-job value, mean launch time, roofline fraction and CPU baseline.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -116,7 +121,7 @@ def cpu_sdpa_dense(torch, tensors, head_axis, causal, flops_per_head, n_total, b
     dt = _median_time(run(n))
     flops = flops_per_head * n
     return {"value": round(flops / dt / 1e12, 5), "unit": "TFLOP/s", "cores": CPU_THREADS,
-            "kind": "port",
+            "kind": "torch_sdpa_cpu",
             "sample": f"torch.nn.functional.scaled_dot_product_attention fp32 on CPU "
                       f"({'autograd backward of ' if backward else ''}{what}), {n} of {n_total} "
                       f"(batch, head) pairs as one [1, {n}, S, D] call, median of 3 after 1 "
@@ -257,7 +262,7 @@ def make_decode(torch):
             b += 1
         dt = time.perf_counter() - t0
         return {"value": round(done / dt / 1e9, 4), "unit": "GB/s", "cores": CPU_THREADS,
-                "kind": "port",
+                "kind": "torch_sdpa_cpu",
                 "sample": f"per sequence: block-table gather + "
                           f"torch.nn.functional.scaled_dot_product_attention(enable_gqa=True), "
                           f"fp32 on CPU, {b} of {B} sequences in {dt:.2f} s (gather included); "
@@ -328,7 +333,7 @@ def make_varlen(torch):
             b += 1
         dt = time.perf_counter() - t0
         return {"value": round(done / dt / 1e12, 5), "unit": "TFLOP/s", "cores": CPU_THREADS,
-                "kind": "port",
+                "kind": "torch_math_cpu",
                 "sample": f"SDPA math in fp32 torch ops on CPU per sequence (scores, ALiBi, "
                           f"softcap, causal + window mask, softmax, PV), {b} of 32 sequences "
                           f"in {dt:.2f} s; torch.set_num_threads({CPU_THREADS})"}
@@ -453,34 +458,87 @@ def measure_traffic(workload, kernels, keep_dir=None):
     return out, None
 
 
+class _HipEvents:
+    """Timing events of the HIP runtime this process runs on, created with
+    ``hipEventReleaseToDevice``: recording one then ends with a device-scope
+    release instead of the default system-scope one (the runtime's flag for
+    precise timings of the commands between events).  torch's events use the
+    default flags; around every decode call their system-scope releases cost
+    about 13 us of GPU time per step (measured on MI355X, 197.5 -> 211 us)."""
+
+    RELEASE_TO_DEVICE = 0x40000000
+
+    def __init__(self):
+        path = next((l.split()[-1] for l in open("/proc/self/maps") if "libamdhip64" in l),
+                    "libamdhip64.so.7")
+        hip = ctypes.CDLL(path)
+        hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                            ctypes.c_void_p]
+        hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        for f in ("hipEventCreateWithFlags", "hipEventRecord", "hipEventElapsedTime",
+                  "hipEventDestroy"):
+            getattr(hip, f).restype = ctypes.c_int
+        self.hip = hip
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed with hipError {rc}")
+
+    def create(self):
+        ev = ctypes.c_void_p()
+        self._ok(self.hip.hipEventCreateWithFlags(ctypes.byref(ev), self.RELEASE_TO_DEVICE),
+                 "hipEventCreateWithFlags")
+        return ev
+
+    def record(self, ev, stream_handle):
+        self._ok(self.hip.hipEventRecord(ev, ctypes.c_void_p(stream_handle)), "hipEventRecord")
+
+    def elapsed_ms(self, start, stop):
+        ms = ctypes.c_float()
+        self._ok(self.hip.hipEventElapsedTime(ctypes.byref(ms), start, stop),
+                 "hipEventElapsedTime")
+        return ms.value
+
+    def destroy(self, ev):
+        self.hip.hipEventDestroy(ev)
+
+
 class _LaunchTimer:
     """Records HIP events on the launch stream around every call of one C-ABI
     entry point (``fa_<name>``, the launch of the dominant kernel).  The
     events bracket the library call itself, so the Python wrapper's argument
     preparation, which the GPU would otherwise wait out when its queue is
     empty (the KV-cache path synchronizes once per call to check its
-    arguments), stays outside the window."""
+    arguments), stays outside the window.  The events are created before the
+    timed region (``_HipEvents``: device-scope release)."""
 
-    def __init__(self, torch, name):
-        self.torch, self.name, self.pairs = torch, name, []
+    def __init__(self, torch, name, calls):
+        self.torch, self.name, self.pairs, self.used = torch, name, [], 0
         self.orig = self.lib = None
+        self.calls = calls
 
     def __enter__(self):
         from flash_attn_triton import _native
         if self.name is None:
             return self
+        self.ev = _HipEvents()
+        self.pairs = [(self.ev.create(), self.ev.create()) for _ in range(self.calls)]
         self.lib = _native.load()
         self.cname = "fa_" + self.name
         self.orig = getattr(self.lib, self.cname)
-        torch, orig, pairs = self.torch, self.orig, self.pairs
+        torch, orig, ev = self.torch, self.orig, self.ev
 
         def timed(*a):
-            stream = torch.cuda.current_stream()
-            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            s.record(stream)
+            if self.used == len(self.pairs):
+                self.pairs.append((ev.create(), ev.create()))
+            s, e = self.pairs[self.used]
+            self.used += 1
+            stream = torch.cuda.current_stream().cuda_stream
+            ev.record(s, stream)
             r = orig(*a)
-            e.record(stream)
-            pairs.append((s, e))
+            ev.record(e, stream)
             return r
 
         setattr(self.lib, self.cname, timed)
@@ -492,8 +550,13 @@ class _LaunchTimer:
         return False
 
     def mean_s(self):
-        ms = [s.elapsed_time(e) for s, e in self.pairs]
-        return sum(ms) / len(ms) / 1e3 if ms else None
+        if not self.used:
+            return None
+        ms = [self.ev.elapsed_ms(s, e) for s, e in self.pairs[:self.used]]
+        for s, e in self.pairs:
+            self.ev.destroy(s)
+            self.ev.destroy(e)
+        return sum(ms) / len(ms) / 1e3
 
 
 def prewarm(torch, step, seconds):
@@ -513,19 +576,30 @@ def prewarm(torch, step, seconds):
 
 def measure(torch, wl, steps, warmup, prewarm_s=0.0):
     """Whole-job time of ``steps`` steps after the clock pre-warm and ``warmup``
-    untimed steps, and the mean launch time of the dominant kernel inside the
-    timed region."""
+    untimed steps, and the mean launch time of the dominant kernel.
+
+    Two timed regions of ``steps`` steps each: the first, with nothing but the
+    steps between its two synchronizations, gives the whole-job value; the
+    second records HIP events around every launch of the dominant kernel and
+    gives its mean launch time.  Events between launches are packets of their
+    own on the stream: around every decode call (a 200 us step) they added
+    about 13 us per step to the whole job, whichever release scope they use."""
     step = wl["step"]
     n_pre = prewarm(torch, step, prewarm_s)
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    with _LaunchTimer(torch, wl["native"]) as timer:
-        t0 = time.perf_counter()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    with _LaunchTimer(torch, wl["native"], steps) as timer:
+        t1 = time.perf_counter()
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
+        wall_events = time.perf_counter() - t1
     avg_launch_s = timer.mean_s()
     if avg_launch_s is None:   # copy calibration: no native entry point
         avg_launch_s = wall / steps
@@ -538,6 +612,7 @@ def measure(torch, wl, steps, warmup, prewarm_s=0.0):
         "achieved": achieved,
         "frac": achieved / wl["peak"],
         "prewarm_steps": n_pre,
+        "ms_per_step_with_events": wall_events / steps * 1e3,
     }
 
 
@@ -550,7 +625,7 @@ def run_cpu(torch, wl, budget):
 
 
 # The other targets of the metric, measured with the headline in the default run.
-EXTRAS = ("dense", "int8_causal", "int8", "decode")
+EXTRAS = ("dense", "int8_causal", "int8", "decode", "varlen")
 
 
 def main():
@@ -603,6 +678,9 @@ def main():
         "traffic": None,
         "kernel": " + ".join(wl["kernels"]),
         "avg_launch_us": round(m["avg_launch_s"] * 1e6, 2),
+        "launch_timing": "HIP events (device-scope release) around every launch in a second "
+                         "timed run of the same steps",
+        "ms_per_step_with_events": round(m["ms_per_step_with_events"], 4),
     }
     if traffic is not None:
         fetch, ffac = traffic["FETCH_SIZE"]
