@@ -36,25 +36,27 @@ hipError_t launch_fwd_cfg(FwdParams p, int rows_for_grid, int outer_blocks, hipS
 // Prefill tile table (fa_prefill_kernel.h), keyed by head dim and by whether
 // the problem is masked (causal, window or varlen):
 //   D = 128, masked  : 4 waves, 32-key tiles, 3 waves per SIMD (165 VGPRs);
-//                      with the generic epilogue 2 waves, 2 per SIMD
+//                      with the generic epilogue 2 waves, 2 per SIMD, tiles
+//                      by LDS-DMA through a 3 K / 2 V stage ring (KS = 3)
 //   D = 128, unmasked: 8 waves (256 query rows share each K/V tile), 64-key tiles
 //   D = 256          : 8 waves, 32-key tiles (the O^T accumulators take 128 VGPRs)
 //   D = 32 / 64      : 4 waves, 64-key tiles
 // Measured on MI355X at B4 H32 S4096 D128: the masked choice is ahead on
 // causal and varlen (less work past the diagonal / sequence end), the
 // unmasked one on non-causal.
-template <class T, int D, int NW, int BN, bool GEN, int WPE, bool BIAS = false>
+template <class T, int D, int NW, int BN, bool GEN, int WPE, bool BIAS = false, int KS = 0>
 hipError_t launch_prefill_cfg(FwdParams p, hipStream_t st) {
   using Tile = PrefillTile<D, NW, BN>;
-  auto kern = prefill_kernel<T, D, NW, BN, GEN, WPE, BIAS>;
+  constexpr int kLds = prefill_lds_bytes<D, NW, BN, KS>();
+  auto kern = prefill_kernel<T, D, NW, BN, GEN, WPE, BIAS, KS>;
   static std::atomic<uint64_t> lds_devices{0};
-  if (hipError_t e = set_lds_limit(lds_devices, kern, Tile::LDS_BYTES); e != hipSuccess) return e;
+  if (hipError_t e = set_lds_limit(lds_devices, kern, kLds); e != hipSuccess) return e;
   p.n_mblocks = (p.seqlen_q + Tile::BM - 1) / Tile::BM;
   const int64_t total = (int64_t)p.n_mblocks * p.heads_q * p.batch;
   if (total <= 0) return hipSuccess;
   if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
   p.total_blocks = (int)total;
-  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), Tile::LDS_BYTES, st, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), kLds, st, p);
   return hipGetLastError();
 }
 
@@ -142,11 +144,16 @@ hipError_t launch_prefill(const FwdParams& p, hipStream_t st) {
     }
     // The generic epilogue (varlen, ALiBi, softcap, window) does not fit the
     // 168-VGPR budget of 3 waves per SIMD without spilling: 2 waves, in
-    // workgroups of 2 (64 rows; measured at BASELINE config 5: 4 % faster
-    // than 4-wave workgroups, which visit more key tiles per row at a window
-    // edge; 3 waves per SIMD spill and were 3.3x slower, 64-key tiles 1.6x).
+    // workgroups of 2 (64 rows; measured at BASELINE config 5 with the tiles
+    // staged through VGPRs: 4 % faster than 4-wave workgroups, which visit
+    // more key tiles per row at a window edge; 3 waves per SIMD spill and
+    // were 3.3x slower, 64-key tiles 1.6x).
+    // The tiles go global -> LDS by LDS-DMA in a ring of 3 K and 2 V stages
+    // (40 KiB: four workgroups per CU).  Measured at BASELINE config 5 on one
+    // MI355X: 884 us against 927 us with the tiles staged through VGPRs; the
+    // 4-wave form with 5 + 4 stages measured 927 us.
     if (masked) {
-      if constexpr (GEN) return launch_prefill_cfg<T, D, 2, 32, GEN, 2>(p, st);
+      if constexpr (GEN) return launch_prefill_cfg<T, D, 2, 32, GEN, 2, false, 3>(p, st);
       else return launch_prefill_cfg<T, D, 4, 32, GEN, 3>(p, st);
     }
     return launch_prefill_cfg<T, D, 8, 64, GEN, 2>(p, st);

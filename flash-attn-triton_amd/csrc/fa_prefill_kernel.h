@@ -26,6 +26,14 @@
 //   O^T += V^T P^T (A = V^T gathered from the row-major V tile with the gfx950
 //   LDS transpose read ds_read_b64_tr_b16, B = P^T from the score
 //   accumulators), K/V double-buffered in LDS, one barrier per tile.
+//
+// KS > 0 (D = 128, 32-key tiles, no attn_bias): the tiles go global -> LDS
+// through the buffer loads' LDS mode instead of VGPR staging, unpadded with
+// the XOR swizzle of the ping-pong kernel (16-byte chunk c of row r at
+// c ^ (r & 15) for K, c ^ 4 (r & 3) for V), in a ring of KS K stages and
+// KS - 1 V stages: the loads of K_{t+KS-1} and V_{t+KS-2} go out at the top
+// of tile t, so K has KS - 1 tiles of compute to land in and V KS - 2 plus
+// the S^T product and softmax of its own tile.
 #pragma once
 
 #include "fa_fwd_kernel.h"
@@ -57,13 +65,23 @@ struct PrefillTile {
   static_assert(CHUNKS % NT == 0 || CHUNKS < NT, "tiles must split evenly over threads");
 };
 
+// Dynamic LDS of prefill_kernel: the padded double buffers, or with KS > 0
+// the K ring (KS tiles) and the V ring (KS - 1 tiles) of unpadded rows.
+template <int D, int NW, int BN, int KS>
+constexpr int prefill_lds_bytes() {
+  return KS > 0 ? (2 * KS - 1) * BN * D * 2 : PrefillTile<D, NW, BN>::LDS_BYTES;
+}
+
 // BIAS: the additive fp32 attn_bias is read in the score epilogue (GENERIC
 // only).  It is a separate instantiation because its per-score loads raise
 // register pressure past the budget of the 3-waves-per-SIMD tiles.
-template <class T, int D, int NW, int BN, bool GENERIC, int WPE, bool BIAS = false>
+template <class T, int D, int NW, int BN, bool GENERIC, int WPE, bool BIAS = false, int KS = 0>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void prefill_kernel(const FwdParams p) {
   static_assert(GENERIC || !BIAS, "the bias is applied by the generic epilogue");
+  constexpr bool kDma = KS > 0;
+  static_assert(!kDma || (D == 128 && BN == 32 && !BIAS && KS >= 3),
+                "the LDS-DMA ring is laid out for head dim 128 and 32-key tiles");
   using Tile = PrefillTile<D, NW, BN>;
   constexpr int BM = Tile::BM;
   constexpr int NT = Tile::NT;
@@ -173,6 +191,7 @@ void prefill_kernel(const FwdParams p) {
   if (wl >= 0) k_lo = max(0, row0 + qoff32 - wl);
   const int t_begin = k_lo / BN;
   const int t_end = k_hi > k_lo ? (k_hi + BN - 1) / BN : t_begin;
+  const int J_all = t_end - t_begin;
 
   // ------------------------------------------------------------ Q^T in VGPRs
   const uint16_t* qg = static_cast<const uint16_t*>(p.q);
@@ -244,6 +263,58 @@ void prefill_kernel(const FwdParams p) {
     }
   };
 
+  // LDS-DMA ring (kDma).  Wave w copies rows [4 (IPW w + i), +4) of every K
+  // and V tile, i < IPW; lane l writes physical chunk l % 16 of row
+  // 4 (IPW w + i) + l / 16, so it loads the logical chunk the swizzle puts
+  // there.  Tiles at or past J get an empty resource: the instruction still
+  // retires (keeping the wait counts uniform) and writes zeros.
+  constexpr int DTILEB = BN * D * 2;                  // bytes of one K or V tile
+  constexpr int IPW = kDma ? DTILEB / 1024 / NW : 1;  // DMA instructions per wave and tile
+  static_assert(!kDma || IPW * NW * 1024 == DTILEB, "tile must split evenly over the waves");
+  uint8_t* const k_ring = reinterpret_cast<uint8_t*>(smem);
+  uint8_t* const v_ring = k_ring + (kDma ? KS : 0) * DTILEB;
+  uint32_t kd_off[IPW], vd_off[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int r = 4 * (IPW * w + i) + (lane >> 4);
+    const int pc = lane & 15;
+    kd_off[i] = (uint32_t)r * k_row_b + (uint32_t)((pc ^ (r & 15)) * 16);
+    vd_off[i] = (uint32_t)r * v_row_b + (uint32_t)((pc ^ (4 * (r & 3))) * 16);
+  }
+  const uint32_t k_ring_a = lds_address(k_ring) + IPW * w * 1024;
+  const uint32_t v_ring_a = lds_address(v_ring) + IPW * w * 1024;
+  auto issue_k = [&](int rel) __attribute__((always_inline)) {
+    const int n0 = (t_begin + rel) * BN;
+    const uint32_t ext = rel < J_all ? rows_extent(n0, Sk, p.k_ss, D) : 0u;
+    const u32x4 rs = make_rsrc_words(kg + (int64_t)(rel < J_all ? n0 : 0) * p.k_ss, ext);
+    const uint32_t dst = k_ring_a + (uint32_t)(rel % (kDma ? KS : 1)) * DTILEB;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, kd_off[i]);
+  };
+  auto issue_v = [&](int rel) __attribute__((always_inline)) {
+    const int n0 = (t_begin + rel) * BN;
+    const uint32_t ext = rel < J_all ? rows_extent(n0, Sk, p.v_ss, D) : 0u;
+    const u32x4 rs = make_rsrc_words(vg + (int64_t)(rel < J_all ? n0 : 0) * p.v_ss, ext);
+    const uint32_t dst = v_ring_a + (uint32_t)(rel % (kDma ? KS - 1 : 1)) * DTILEB;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, vd_off[i]);
+  };
+  // Swizzled operand reads of the ring: K (16 B per lane) row kb*32 + c32,
+  // logical chunk 2 kc + g; V^T (ds_read_b64_tr_b16) as vt_lane below.
+  uint32_t kd_rd[NKC], vd_rd[NDB];
+  {
+    const int j16 = lane & 15;
+    const uint32_t v_rd = (uint32_t)(4 * g + (j16 >> 2)) * (D * 2) + (uint32_t)((j16 & 1) * 8);
+    const int v_cx = 2 * (c32 >> 4) + ((j16 & 3) >> 1);
+    const int v_sw = j16 >> 2;
+#pragma unroll
+    for (int kc = 0; kc < NKC; ++kc)
+      kd_rd[kc] = (uint32_t)c32 * (D * 2) + ((uint32_t)(2 * kc + g) ^ (uint32_t)(c32 & 15)) * 16;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+      vd_rd[db] = v_rd + ((((uint32_t)db ^ (uint32_t)v_sw) << 2) + (uint32_t)v_cx) * 16;
+  }
+
   // V^T operand of O^T += V^T P^T through ds_read_b64_tr_b16.  Within each
   // 16-lane group the instruction returns to lane i the i-th column of the 4x16
   // block whose row r is read by lanes 4r..4r+3 (4 elements each).  Lane
@@ -292,7 +363,10 @@ void prefill_kernel(const FwdParams p) {
       sd[kb] = cinit;
 #pragma unroll
       for (int kc = 0; kc < NKC; ++kc) {
-        const u32x4 a = load16(Ks + (kb * 32 + c32) * KSTR + kc * 16 + g * 8);
+        const u32x4 a =
+            kDma ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint8_t*>(Ks) +
+                                                  kd_rd[kc] + kb * 32 * D * 2)
+                 : load16(Ks + (kb * 32 + c32) * KSTR + kc * 16 + g * 8);
         sd[kb] = T::mfma32(a, qreg[kc], sd[kb]);
       }
     }
@@ -303,9 +377,12 @@ void prefill_kernel(const FwdParams p) {
     for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        const uint16_t* vp = Vs + vt_lane + cc * 16 * VSTR + db * 32;
+        const uint16_t* vp =
+            kDma ? reinterpret_cast<const uint16_t*>(reinterpret_cast<const uint8_t*>(Vs) +
+                                                     vd_rd[db] + cc * 16 * D * 2)
+                 : Vs + vt_lane + cc * 16 * VSTR + db * 32;
         const u32x2 lo = lds_read_tr16(vp);
-        const u32x2 hi = lds_read_tr16(vp + 8 * VSTR);
+        const u32x2 hi = lds_read_tr16(vp + 8 * (kDma ? D : VSTR));
         const u32x4 a = {lo[0], lo[1], hi[0], hi[1]};
         acc[db] = T::mfma32(a, pb[cc], acc[db]);
       }
@@ -522,18 +599,48 @@ void prefill_kernel(const FwdParams p) {
   auto compute = [&](int it) __attribute__((always_inline)) {
     const int n0 = (t_begin + it) * BN;
     if (n0 <= kw_hi && n0 + BN - 1 >= kw_lo) {
-      qk(k_slot(it), s);
+      const uint16_t* Ks = kDma ? reinterpret_cast<const uint16_t*>(k_ring + (it % (kDma ? KS : 1)) * DTILEB)
+                                : k_slot(it);
+      const uint16_t* Vs = kDma ? reinterpret_cast<const uint16_t*>(v_ring + (it % (kDma ? KS - 1 : 1)) * DTILEB)
+                                : v_slot(it);
+      qk(Ks, s);
       softmax_tile(s, n0, n0 < kf_lo, n0 + BN - 1 > kf_hi, pbuf);
-      pv(v_slot(it), pbuf);
+      pv(Vs, pbuf);
     }
   };
-  if (J > 0) {
+  if constexpr (kDma) {
+    // Prologue: K_0, V_0, ..., K_{KS-3}, V_{KS-3}, K_{KS-2}; tile it then
+    // issues V_{it+KS-2} and K_{it+KS-1}.  At the top of tile it the loads
+    // issued after K_it and V_it are those of 2 KS - 5 tiles (K_{it+1},
+    // V_{it+1}, ..., K_{it+KS-2}): waiting until at most that many remain
+    // makes this wave's part of tile it visible, and the barrier everyone's.
+    // The slots refilled in tile it held K_{it-1} and V_{it-1}, whose reads
+    // every wave finished before that barrier.
+#pragma unroll
+    for (int i = 0; i < KS - 2; ++i) {
+      issue_k(i);
+      issue_v(i);
+    }
+    issue_k(KS - 2);
+    for (int it = 0; it < J; ++it) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((2 * KS - 5) * IPW));
+      __builtin_amdgcn_s_barrier();
+      issue_v(it + KS - 2);
+      issue_k(it + KS - 1);
+      compute(it);
+    }
+    // Every load (including the empty ones past the last tile) has landed
+    // before the ring is reused for the output staging below.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  } else if (J > 0) {
     load_k(t_begin, kreg);
     load_v(t_begin, vreg);
     store_k(0, kreg);
     store_v(0, vreg);
   }
-  if constexpr (kDeep) {
+  if constexpr (kDma) {
+    // (the ring loop above)
+  } else if constexpr (kDeep) {
     // Tile it + 1 waits in one register set while tile it + 2 loads into the
     // other; the sets alternate, so the loop runs tiles in pairs.
     if (J > 1) {
@@ -584,7 +691,8 @@ void prefill_kernel(const FwdParams p) {
     // accumulators, each instruction wrote 8 bytes of 32 rows, and the
     // partial lines reached HBM piecemeal (measured at BASELINE config 5:
     // 290.6 MB written for a 134.2 MB output).
-    static_assert(NW * kStageOutBytes <= Tile::LDS_BYTES, "output staging must fit the tile area");
+    static_assert(NW * kStageOutBytes <= prefill_lds_bytes<D, NW, BN, KS>(),
+                  "output staging must fit the tile area");
     __syncthreads();
     if (wave_active)
       stage_rows_store<T, NDB>(acc, inv_l, reinterpret_cast<uint8_t*>(smem) + w * kStageOutBytes,
