@@ -206,8 +206,6 @@ int bwd_check_common(const char* name, const void* q, const void* k, const void*
   if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256)
     return fail(FA_ERR_UNSUPPORTED, "%s: head_dim %lld not in {32,64,128,256}", name,
                 (long long)head_dim);
-  if (dtype == FA_DTYPE_F32 && head_dim > 128)
-    return fail(FA_ERR_UNSUPPORTED, "%s: the fp32 backward supports head_dim 32, 64 and 128", name);
   if (heads_q <= 0 || heads_k <= 0 || heads_q % heads_k != 0)
     return fail(FA_ERR_INVALID, "%s: bad head counts Hq=%lld Hk=%lld", name, (long long)heads_q,
                 (long long)heads_k);

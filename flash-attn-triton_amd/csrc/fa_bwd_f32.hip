@@ -27,8 +27,12 @@
 //   one key in each lane, so F P and dS are the B operands of dV^T += dO^T (F P)
 //   and dK^T += Q^T dS.
 // No atomics except for the attn_bias gradient (broadcast dims sum).  Head
-// dims 32, 64 and 128 (16 is run at 32 by the caller): at 256 the Q^T / dO^T
-// (or K^T / V^T) registers alone would take every VGPR.
+// dims 32, 64, 128 and 256 (16 is run at 32 by the caller).  At 256 the
+// resident Q^T / dO^T (or K^T / V^T) rows take 256 registers per lane, and
+// the full-width accumulators another 128 (dQ) or 256 (dK and dV): each
+// kernel then makes two passes over its tiles, accumulating and storing
+// output dims [0, 128) in the first and [128, 256) in the second, and
+// recomputes S and dP in each (one wave per SIMD, 512 registers).
 #include "fa_bwd.h"
 
 namespace fa {
@@ -78,6 +82,8 @@ void bwd_f32_dq_kernel(const BwdParams p) {
   constexpr int BB = Tile::BB, TN = Tile::TN, STR = Tile::STR, NT = Tile::NT;
   constexpr int CPR = Tile::CPR, CH = Tile::CH, CPT = Tile::CPT;
   constexpr int DH = D / 2, NDB = D / 32;
+  constexpr int NPASS = D > 128 ? 2 : 1;   // passes over the output dims
+  constexpr int NDBP = NDB / NPASS;        // 32-dim output blocks per pass
 
   extern __shared__ __attribute__((aligned(16))) float smf[];
   float* Ks = smf;
@@ -173,10 +179,13 @@ void bwd_f32_dq_kernel(const BwdParams p) {
 
   const float* kg = static_cast<const float*>(p.k) + f32_row_base(p, p.k_sb, p.k_ss, p.k_sh, b, kvh, ks);
   const float* vg = static_cast<const float*>(p.v) + f32_row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks);
+  float* dqrow = static_cast<float*>(p.dq) + f32_row_base(p, p.dq_sb, p.dq_ss, p.dq_sh, b, hh, qs) +
+                 (int64_t)qi * p.dq_ss;
 
-  f32x16 acc[NDB];
+  for (int pass = 0; pass < NPASS; ++pass) {
+  f32x16 acc[NDBP];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) acc[db] = f32x16{};
+  for (int db = 0; db < NDBP; ++db) acc[db] = f32x16{};
 
   for (int t = t_begin; t < t_end; ++t) {
     const int n0 = t * TN;
@@ -226,33 +235,36 @@ void bwd_f32_dq_kernel(const BwdParams p) {
       if (GENERIC && p.drop.enabled && vis) dpv *= dropout_factor_at(p.drop, qi, key, hh, b);
       const float ds = pr * (dpv - delta) * cg;
       dsv[v] = ds;
-      if (BIAS && dbias_row != nullptr && ds != 0.f) atomicAdd(dbias_row + (int64_t)key * p.dbias_sk, ds);
+      // dS is the same in every pass: the bias gradient takes it once.
+      if (BIAS && pass == 0 && dbias_row != nullptr && ds != 0.f)
+        atomicAdd(dbias_row + (int64_t)key * p.dbias_sk, ds);
     }
 
-    // dQ^T += K^T dS^T.
+    // dQ^T += K^T dS^T (this pass's output dims).
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
+    for (int dbl = 0; dbl < NDBP; ++dbl) {
+      const int db = pass * NDBP + dbl;
 #pragma unroll
       for (int jj = 0; jj < 16; ++jj) {
         const int key = 8 * (jj >> 2) + 4 * g + (jj & 3);
-        acc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[key * STR + db * 32 + c32], dsv[jj], acc[db], 0, 0, 0);
+        acc[dbl] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[key * STR + db * 32 + c32], dsv[jj], acc[dbl], 0, 0, 0);
       }
     }
   }
 
-  if (!row_valid) return;
-  float* dqrow = static_cast<float*>(p.dq) + f32_row_base(p, p.dq_sb, p.dq_ss, p.dq_sh, b, hh, qs) +
-                 (int64_t)qi * p.dq_ss;
+  if (row_valid) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
+    for (int dbl = 0; dbl < NDBP; ++dbl) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = db * 32 + r * 8 + g * 4;
-      *reinterpret_cast<f32x4*>(dqrow + d) =
-          f32x4{acc[db][4 * r] * p.scale, acc[db][4 * r + 1] * p.scale, acc[db][4 * r + 2] * p.scale,
-                acc[db][4 * r + 3] * p.scale};
+      for (int r = 0; r < 4; ++r) {
+        const int d = (pass * NDBP + dbl) * 32 + r * 8 + g * 4;
+        *reinterpret_cast<f32x4*>(dqrow + d) =
+            f32x4{acc[dbl][4 * r] * p.scale, acc[dbl][4 * r + 1] * p.scale,
+                  acc[dbl][4 * r + 2] * p.scale, acc[dbl][4 * r + 3] * p.scale};
+      }
     }
   }
+  }   // pass
 }
 
 template <int D, bool GENERIC, bool VARLEN, bool BIAS>
@@ -263,6 +275,8 @@ void bwd_f32_dkdv_kernel(const BwdParams p) {
   constexpr int BB = Tile::BB, TN = Tile::TN, STR = Tile::STR, NT = Tile::NT;
   constexpr int CPR = Tile::CPR, CH = Tile::CH, CPT = Tile::CPT;
   constexpr int DH = D / 2, NDB = D / 32;
+  constexpr int NPASS = D > 128 ? 2 : 1;   // passes over the output dims
+  constexpr int NDBP = NDB / NPASS;        // 32-dim output blocks per pass
 
   extern __shared__ __attribute__((aligned(16))) float smf[];
   float* Qs = smf;
@@ -297,22 +311,27 @@ void bwd_f32_dkdv_kernel(const BwdParams p) {
   const bool causal = p.causal != 0;
   const int wl = p.window_left, wr = p.window_right;
 
-  // K^T, V^T of this lane's key.
-  float kv[DH], vv[DH];
+  // K^T, V^T of this lane's key.  D = 256: only K^T stays in registers; the
+  // lane's V row is read again (from L2) in two halves for every query tile
+  // (dP = dO V^T is its only use), which keeps K^T, the accumulators of one
+  // output half and the tile's S / dP / P / dS within the 512 registers.
+  constexpr bool kVres = D <= 128;
+  float kv[DH], vv[kVres ? DH : 1];
+  const float* vrow = static_cast<const float*>(p.v) +
+                      f32_row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks) + (int64_t)kj * p.v_ss + g * DH;
   {
     const float* krow = static_cast<const float*>(p.k) +
                         f32_row_base(p, p.k_sb, p.k_ss, p.k_sh, b, kvh, ks) + (int64_t)kj * p.k_ss + g * DH;
-    const float* vrow = static_cast<const float*>(p.v) +
-                        f32_row_base(p, p.v_sb, p.v_ss, p.v_sh, b, kvh, ks) + (int64_t)kj * p.v_ss + g * DH;
 #pragma unroll
     for (int j = 0; j < DH; j += 4) {
       const f32x4 z = {0.f, 0.f, 0.f, 0.f};
       const f32x4 xk = key_valid ? *reinterpret_cast<const f32x4*>(krow + j) : z;
-      const f32x4 xv = key_valid ? *reinterpret_cast<const f32x4*>(vrow + j) : z;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        kv[j + e] = xk[e];
-        vv[j + e] = xv[e];
+      for (int e = 0; e < 4; ++e) kv[j + e] = xk[e];
+      if constexpr (kVres) {
+        const f32x4 xv = key_valid ? *reinterpret_cast<const f32x4*>(vrow + j) : z;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vv[j + e] = xv[e];
       }
     }
   }
@@ -328,9 +347,15 @@ void bwd_f32_dkdv_kernel(const BwdParams p) {
   const int m_begin = (int)(q_lo / TN);
   const int m_end = q_hi > q_lo ? (int)((q_hi + TN - 1) / TN) : m_begin;
 
-  f32x16 dk[NDB], dvacc[NDB];
+  float* dkrow = static_cast<float*>(p.dk) + f32_row_base(p, p.dk_sb, p.dk_ss, p.dk_sh, b, kvh, ks) +
+                 (int64_t)kj * p.dk_ss;
+  float* dvrow = static_cast<float*>(p.dv) + f32_row_base(p, p.dv_sb, p.dv_ss, p.dv_sh, b, kvh, ks) +
+                 (int64_t)kj * p.dv_ss;
+
+  for (int pass = 0; pass < NPASS; ++pass) {
+  f32x16 dk[NDBP], dvacc[NDBP];
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
+  for (int db = 0; db < NDBP; ++db) {
     dk[db] = f32x16{};
     dvacc[db] = f32x16{};
   }
@@ -374,14 +399,43 @@ void bwd_f32_dkdv_kernel(const BwdParams p) {
       f32x16 s = f32x16{}, dp = f32x16{};
       const float* qrow = Qs + c32 * STR + g * DH;
       const float* drow = Ds + c32 * STR + g * DH;
+      if constexpr (kVres) {
 #pragma unroll
-      for (int j = 0; j < DH; j += 4) {
-        const f32x4 qx = *reinterpret_cast<const f32x4*>(qrow + j);
-        const f32x4 dx = *reinterpret_cast<const f32x4*>(drow + j);
+        for (int j = 0; j < DH; j += 4) {
+          const f32x4 qx = *reinterpret_cast<const f32x4*>(qrow + j);
+          const f32x4 dx = *reinterpret_cast<const f32x4*>(drow + j);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s = __builtin_amdgcn_mfma_f32_32x32x2f32(qx[e], kv[j + e], s, 0, 0, 0);
-          dp = __builtin_amdgcn_mfma_f32_32x32x2f32(dx[e], vv[j + e], dp, 0, 0, 0);
+          for (int e = 0; e < 4; ++e) {
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(qx[e], kv[j + e], s, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x2f32(dx[e], vv[j + e], dp, 0, 0, 0);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < DH; j += 4) {
+          const f32x4 qx = *reinterpret_cast<const f32x4*>(qrow + j);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(qx[e], kv[j + e], s, 0, 0, 0);
+        }
+        constexpr int VH = DH / 2;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float vh[VH];
+#pragma unroll
+          for (int j = 0; j < VH; j += 4) {
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 xv = key_valid ? *reinterpret_cast<const f32x4*>(vrow + h * VH + j) : z;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vh[j + e] = xv[e];
+          }
+#pragma unroll
+          for (int j = 0; j < VH; j += 4) {
+            const f32x4 dx = *reinterpret_cast<const f32x4*>(drow + h * VH + j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              dp = __builtin_amdgcn_mfma_f32_32x32x2f32(dx[e], vh[j + e], dp, 0, 0, 0);
+          }
         }
       }
 
@@ -409,36 +463,36 @@ void bwd_f32_dkdv_kernel(const BwdParams p) {
         dsv[v] = pr * (dp[v] * f - Es[rr]) * cg;
       }
 
-      // dV^T += dO^T (F P), dK^T += Q^T dS.
+      // dV^T += dO^T (F P), dK^T += Q^T dS (this pass's output dims).
 #pragma unroll
-      for (int db = 0; db < NDB; ++db) {
+      for (int dbl = 0; dbl < NDBP; ++dbl) {
+        const int db = pass * NDBP + dbl;
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) {
           const int rr = 8 * (jj >> 2) + 4 * g + (jj & 3);
-          dvacc[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ds[rr * STR + db * 32 + c32], pv[jj], dvacc[db], 0, 0, 0);
-          dk[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[rr * STR + db * 32 + c32], dsv[jj], dk[db], 0, 0, 0);
+          dvacc[dbl] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ds[rr * STR + db * 32 + c32], pv[jj], dvacc[dbl], 0, 0, 0);
+          dk[dbl] = __builtin_amdgcn_mfma_f32_32x32x2f32(Qs[rr * STR + db * 32 + c32], dsv[jj], dk[dbl], 0, 0, 0);
         }
       }
     }
   }
 
-  if (!key_valid) return;
-  float* dkrow = static_cast<float*>(p.dk) + f32_row_base(p, p.dk_sb, p.dk_ss, p.dk_sh, b, kvh, ks) +
-                 (int64_t)kj * p.dk_ss;
-  float* dvrow = static_cast<float*>(p.dv) + f32_row_base(p, p.dv_sb, p.dv_ss, p.dv_sh, b, kvh, ks) +
-                 (int64_t)kj * p.dv_ss;
+  if (key_valid) {
 #pragma unroll
-  for (int db = 0; db < NDB; ++db) {
+    for (int dbl = 0; dbl < NDBP; ++dbl) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int d = db * 32 + r * 8 + g * 4;
-      *reinterpret_cast<f32x4*>(dkrow + d) =
-          f32x4{dk[db][4 * r] * p.scale, dk[db][4 * r + 1] * p.scale, dk[db][4 * r + 2] * p.scale,
-                dk[db][4 * r + 3] * p.scale};
-      *reinterpret_cast<f32x4*>(dvrow + d) =
-          f32x4{dvacc[db][4 * r], dvacc[db][4 * r + 1], dvacc[db][4 * r + 2], dvacc[db][4 * r + 3]};
+      for (int r = 0; r < 4; ++r) {
+        const int d = (pass * NDBP + dbl) * 32 + r * 8 + g * 4;
+        *reinterpret_cast<f32x4*>(dkrow + d) =
+            f32x4{dk[dbl][4 * r] * p.scale, dk[dbl][4 * r + 1] * p.scale,
+                  dk[dbl][4 * r + 2] * p.scale, dk[dbl][4 * r + 3] * p.scale};
+        *reinterpret_cast<f32x4*>(dvrow + d) =
+            f32x4{dvacc[dbl][4 * r], dvacc[dbl][4 * r + 1], dvacc[dbl][4 * r + 2],
+                  dvacc[dbl][4 * r + 3]};
+      }
     }
   }
+  }   // pass
 }
 
 template <int D, bool GEN, bool VARLEN, bool BIAS>
@@ -483,6 +537,7 @@ hipError_t fa_launch_bwd_f32(const fa::BwdParams& p, int head_dim, bool generic,
     FA_F32B_CASE(32)
     FA_F32B_CASE(64)
     FA_F32B_CASE(128)
+    FA_F32B_CASE(256)
     default:
       return hipErrorInvalidValue;
   }

@@ -22,8 +22,7 @@ defect or a host-side copy, never changes a correct result):
   are reduced in the kernel, not with atomics) for dense, cross and varlen
   calls in fp16 / bf16 / fp32, ``attn_bias``, seqused / paged varlen and
   the KV-cache path, which, when gradients are needed, gathers each
-  sequence's keys as the reference does and runs the dense kernels; fp32 at
-  head dim 256 is forward only (``backward`` raises ``NotImplementedError``);
+  sequence's keys as the reference does and runs the dense kernels;
 * dropout draws its mask from a counter-based Philox4x32-10 generator keyed
   by a seed from torch's default CPU generator, one independent mask per
   (batch, head) (the reference's ``tl.rand`` offsets repeat the same mask for

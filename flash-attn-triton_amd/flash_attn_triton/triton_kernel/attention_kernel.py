@@ -13,12 +13,10 @@ directly, so nothing is padded, repeated or copied on the host.
 Autograd: when q, k or v (or the dense path's ``attn_bias``) requires grad
 the forward also keeps the LSE and the backward runs ``fa_bwd_dense`` /
 ``fa_bwd_varlen`` (the reference's ``_attention.backward`` :1185-1198 and
-``_attention_varlen.backward`` :1322-1361): fp16 and bf16, and fp32 at head
-dims up to 128; the bias gradient
+``_attention_varlen.backward`` :1322-1361): fp16, bf16 and fp32 at every head
+dim; the bias gradient
 is dS summed over the bias's broadcast dimensions, as torch autograd gives it
-for the reference's math path (flash_attn_interface.py:15-49).  Not
-differentiable (backward raises ``NotImplementedError``): fp32 at head dim 256
-and the KV-cache path.  Dropout (``dropout_p > 0``) drops probabilities with the
+for the reference's math path (flash_attn_interface.py:15-49).  Dropout (``dropout_p > 0``) drops probabilities with the
 counter-based Philox mask of the kernels; the seed is drawn from torch's
 default CPU generator unless given, and the backward replays the same mask.
 """
@@ -145,13 +143,6 @@ def _f32_alibi(alibi, device):
     return None if alibi is None else alibi.to(device=device, dtype=torch.float32).contiguous()
 
 
-def _check_f32_head_dim(q: torch.Tensor) -> None:
-    if q.dtype == torch.float32 and q.shape[-1] > 128:
-        raise NotImplementedError(
-            "flash_attn_triton (gfx950 HIP build): the fp32 backward supports head dims up to "
-            "128")
-
-
 def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: bool,
                    q_pos_offset: int = 0, window_left: int = -1, window_right: int = -1,
                    softcap: float = 0.0, alibi: Optional[torch.Tensor] = None,
@@ -163,7 +154,6 @@ def dense_backward(q, k, v, out, dout, lse, *, softmax_scale: float, causal: boo
     ``bias``: the forward's fp32 ``[B, Hq, Sq, Sk]`` view; ``dbias`` (optional):
     a zero-filled fp32 view of the same shape whose broadcast dims have stride
     0, which receives the bias gradient."""
-    _check_f32_head_dim(q)
     if q.shape[-1] == 16:
         grads = dense_backward(*(_pad_head_dim(t, 32) for t in (q, k, v, out, dout)), lse,
                                softmax_scale=softmax_scale, causal=causal,
@@ -191,7 +181,6 @@ def varlen_backward(q, k, v, out, dout, lse, cu_q, cu_k, max_seqlen_q: int, max_
                     dropout_seed: int = 0):
     """Gradients ``(dq, dk, dv)`` of ``varlen_forward`` (``fa_bwd_varlen``).
     Rows outside every sequence get zero gradients."""
-    _check_f32_head_dim(q)
     if q.shape[-1] == 16:
         grads = varlen_backward(*(_pad_head_dim(t, 32) for t in (q, k, v, out, dout)), lse,
                                 cu_q, cu_k, max_seqlen_q, max_seqlen_k,

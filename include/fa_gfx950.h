@@ -139,8 +139,8 @@ int fa_fwd_varlen(const void* q, const void* k, const void* v, void* out, float*
  * score options (scale, causal, q_pos_offset, window, softcap, ALiBi,
  * attn_bias) must be those of the forward call.  dq / dk / dv are written, not
  * accumulated; grouped KV heads are reduced inside the kernel (no atomics,
- * deterministic).  dtype fp16 or bf16 (head_dim 32, 64, 128 or 256) or fp32
- * (head_dim 32, 64 or 128; the reference's Triton backward is dtype-generic,
+ * deterministic).  dtype fp16, bf16 or fp32, head_dim 32, 64, 128 or 256
+ * (the reference's Triton backward is dtype-generic,
  * attention_kernel.py:1104-1198).
  *
  * attn_bias / bias_stride[4]: the forward's fp32 bias (may be null).  dbias /

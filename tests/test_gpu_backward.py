@@ -296,19 +296,24 @@ def test_kvcache_gradients_rotary_alibi_window():
     _kvcache_grad_case(False, False, rotary=True, window=(16, 8), seed=340)
 
 
-def test_forward_only_paths_raise_on_backward():
-    # fp32 at head dim 256 has no backward (its K^T / V^T registers would not fit).
-    from flash_attn_triton import flash_attn_func
-    q = randn((1, 64, 2, 256), 100, torch.float32).to(DEV).requires_grad_()
-    out = flash_attn_func(q, q, q)
-    with pytest.raises(NotImplementedError):
-        out.sum().backward()
-
-
-@pytest.mark.parametrize("d", [16, 32, 64, 128])
+@pytest.mark.parametrize("d", [16, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_fp32_head_dims(d, causal):
+    # D = 256: two passes over the output dims in both kernels, V rows read
+    # again per query tile in the dK/dV kernel.
     _dense_case(2, 150, 150, 4, 2, d, dtype=torch.float32, causal=causal, seed=140 + d)
+
+
+def test_fp32_head_dim_256_features():
+    # D = 256 through the generic instantiations: cross lengths, window,
+    # softcap, ALiBi; varlen with ragged sequences; attn_bias (dropout at
+    # D = 256 in fp32: test_gpu_dropout.py).
+    _dense_case(1, 70, 301, 4, 2, 256, dtype=torch.float32, causal=True, window=(64, 0),
+                softcap=20.0, alibi=True, seed=410)
+    _varlen_case([1, 130, 64, 97], [3, 130, 200, 97], Hq=4, Hk=2, D=256,
+                 dtype=torch.float32, causal=True, seed=412)
+    _bias_case((1, 4, 100, 100), Sq=100, Sk=100, D=256, dtype=torch.float32, causal=True,
+               seed=413)
 
 
 def test_fp32_cross_and_features():

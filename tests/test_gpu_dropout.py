@@ -74,6 +74,7 @@ def test_fp32_forward():
 def test_fp32_forward_and_backward():
     _dense(2, 130, 150, 4, 2, 64, 0.4, 31, dtype=torch.float32, causal=True)
     _dense(1, 200, 200, 2, 1, 128, 0.2, 32, dtype=torch.float32, causal=False, softcap=10.0)
+    _dense(1, 96, 96, 2, 1, 256, 0.2, 33, dtype=torch.float32, causal=False)
 
 
 def test_same_seed_same_output_and_seeds_differ():
