@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fa_fastdiv.h"
+
 #include <atomic>
 
 namespace fa {

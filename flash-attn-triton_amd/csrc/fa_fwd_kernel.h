@@ -77,8 +77,11 @@ struct FwdParams {
   int num_splits, split_tiles;
   float* o_part; float* lse_part;
   int n_mblocks, total_blocks, heavy_first;
-  // prefill_persist_kernel: row blocks per workgroup.
+  // prefill_persist_kernel: row blocks per workgroup, and divisions by the
+  // row blocks (causal: pairs of row blocks) per group, the query heads and
+  // the GQA group size (set by the persistent launchers).
   int persist_rounds;
+  FastDiv fd_blk, fd_heads, fd_group;
   // Dropout of the probabilities (prefill, GENERIC instantiations only).
   DropoutCfg drop;
 };

@@ -109,6 +109,9 @@ hipError_t launch_prefill_persist(FwdParams p, hipStream_t st, bool* launched) {
   if (slots * 4 < max_slots * 3 || rounds < 2 || n_mb > (1 << 20)) return hipSuccess;
   p.n_mblocks = (int)n_mb;
   p.persist_rounds = (int)rounds;
+  p.fd_blk = make_fastdiv((uint32_t)(causal ? n_mb / 2 : n_mb));
+  p.fd_heads = make_fastdiv((uint32_t)p.heads_q);
+  p.fd_group = make_fastdiv((uint32_t)p.group);
   auto kern = causal ? prefill_persist_kernel<T, D, true> : prefill_persist_kernel<T, D, false>;
   static std::atomic<uint64_t> lds_devices_c{0}, lds_devices_n{0};
   e = set_lds_limit(causal ? lds_devices_c : lds_devices_n, kern, Tile::LDS_BYTES);

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fa_fastdiv.h"
+
 namespace fa {
 
 // x >= 0 ? floor(x + 0.5) : ceil(x - 0.5) in fp32 (the reference's _round_i8,
@@ -63,6 +65,9 @@ struct Int8Params {
   int causal, seq_len_k, seq_len_q;
   int n_mblocks, total_blocks;
   int persist_rounds;   // int8_persist_kernel: row blocks per workgroup
+  // int8_persist_kernel: divisions by the row blocks (causal: pairs) per
+  // group and by the head count (set by its launcher).
+  FastDiv fd_blk, fd_heads;
 };
 
 }  // namespace fa

@@ -514,6 +514,8 @@ hipError_t launch_int8_persist(Int8Params p, hipStream_t st, bool* launched) {
   if (slots * 4 < max_slots * 3 || rounds < 2 || n_mb > (1 << 20)) return hipSuccess;
   p.n_mblocks = (int)n_mb;
   p.persist_rounds = (int)rounds;
+  p.fd_blk = make_fastdiv((uint32_t)(causal ? n_mb / 2 : n_mb));
+  p.fd_heads = make_fastdiv((uint32_t)p.heads);
   auto kern = causal ? int8_persist_kernel<D, true> : int8_persist_kernel<D, false>;
   static std::atomic<uint64_t> lds_devices_c{0}, lds_devices_n{0};
   e = set_lds_limit(causal ? lds_devices_c : lds_devices_n, kern, Tile::LDS_BYTES);

@@ -102,18 +102,21 @@ void int8_persist_kernel(const Int8Params p) {
   const int rounds = p.persist_rounds;      // row blocks per workgroup
   const int S = p.seqlen;
   // Block r of this workgroup: (batch, head) group gi and first row row0.
+  // Divisions by multiply-high and shift (fd_blk, fd_heads): as runtime
+  // divisions they were a few hundred scalar instructions per descriptor.
   auto make_blk = [&](int r, int& gi, int& row0, int& J) __attribute__((always_inline)) {
     int mb;
     if (CAUSAL) {
-      const int half = n_mb >> 1;
       const int u = (r >> 1) * slots + slot;
-      const int j = u % half;
-      gi = xcd * gx + u / half;
+      const int uq = (int)fdiv((uint32_t)u, p.fd_blk);
+      const int j = u - uq * (n_mb >> 1);
+      gi = xcd * gx + uq;
       mb = (r & 1) ? j : n_mb - 1 - j;
     } else {
       const int u = r * slots + slot;
-      gi = xcd * gx + u / n_mb;
-      mb = u % n_mb;
+      const int uq = (int)fdiv((uint32_t)u, p.fd_blk);
+      gi = xcd * gx + uq;
+      mb = u - uq * n_mb;
     }
     row0 = mb * BM;
     J = CAUSAL ? (mb + 1) * TPB : S / BN;
@@ -121,13 +124,16 @@ void int8_persist_kernel(const Int8Params p) {
   // Element offsets of group gi's Q / V / O rows (the [B, H, S, D] strides)
   // and its K8 (bytes) and key-scale (floats) rows.
   auto q_base_of = [&](int gi) __attribute__((always_inline)) {
-    return (int64_t)(gi / p.heads) * p.q_sb + (int64_t)(gi % p.heads) * p.q_sh;
+    const int b = (int)fdiv((uint32_t)gi, p.fd_heads);
+    return (int64_t)b * p.q_sb + (int64_t)(gi - b * p.heads) * p.q_sh;
   };
   auto o_base_of = [&](int gi) __attribute__((always_inline)) {
-    return (int64_t)(gi / p.heads) * p.o_sb + (int64_t)(gi % p.heads) * p.o_sh;
+    const int b = (int)fdiv((uint32_t)gi, p.fd_heads);
+    return (int64_t)b * p.o_sb + (int64_t)(gi - b * p.heads) * p.o_sh;
   };
   auto v_base_of = [&](int gi) __attribute__((always_inline)) {
-    return (int64_t)(gi / p.heads) * p.v_sb + (int64_t)(gi % p.heads) * p.v_sh;
+    const int b = (int)fdiv((uint32_t)gi, p.fd_heads);
+    return (int64_t)b * p.v_sb + (int64_t)(gi - b * p.heads) * p.v_sh;
   };
   int r_cur = 0;
   int c_gi = 0, c_row0 = 0, c_J = 0;

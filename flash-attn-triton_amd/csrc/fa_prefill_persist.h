@@ -85,21 +85,25 @@ void prefill_persist_kernel(const FwdParams p) {
   auto make_blk = [&](int r, int64_t& q_base, int64_t& o_base, int64_t& lse_base,
                       int64_t& k_base, int64_t& v_base, int& row0, int& J)
       __attribute__((always_inline)) {
+    // The divisions go through fd_blk / fd_heads / fd_group (multiply-high and
+    // shift): as runtime divisions they were a few hundred scalar instructions
+    // per descriptor, and a block change computes five descriptors.
     int gi, mb;
     if (CAUSAL) {
-      const int half = n_mb >> 1;
       const int u = (r >> 1) * slots + slot;
-      const int j = u % half;
-      gi = xcd * gx + u / half;
+      const int uq = (int)fdiv((uint32_t)u, p.fd_blk);
+      const int j = u - uq * (n_mb >> 1);
+      gi = xcd * gx + uq;
       mb = (r & 1) ? j : n_mb - 1 - j;
     } else {
       const int u = r * slots + slot;
-      gi = xcd * gx + u / n_mb;
-      mb = u % n_mb;
+      const int uq = (int)fdiv((uint32_t)u, p.fd_blk);
+      gi = xcd * gx + uq;
+      mb = u - uq * n_mb;
     }
-    const int hh = gi % p.heads_q;
-    const int b = gi / p.heads_q;
-    const int kvh = hh / p.group;
+    const int b = (int)fdiv((uint32_t)gi, p.fd_heads);
+    const int hh = gi - b * p.heads_q;
+    const int kvh = (int)fdiv((uint32_t)hh, p.fd_group);
     q_base = (int64_t)b * p.q_sb + (int64_t)hh * p.q_sh;
     o_base = (int64_t)b * p.o_sb + (int64_t)hh * p.o_sh;
     lse_base = (int64_t)b * p.lse_sb + (int64_t)hh * p.lse_sh;
