@@ -100,3 +100,68 @@ def test_noalloc_batched_cache_two_calls():
     vc2 = randn((2, 1024, hk, d), 711)
     q2 = randn((2, 10, hq, d), 712)
     _check(q2, kc2, vc2, lens2, None, 1024, "batched call 2", causal=True)
+
+
+def test_noalloc_under_graph_capture_replays():
+    # The entry point for code under HIP graph capture: captured once, replayed
+    # with new cache lengths written into the captured length buffer (eager
+    # work and a synchronization between replays); every replay equals an
+    # eager fa_fwd_kvcache call on the same inputs bit for bit.
+    from flash_attn_triton import _native
+    page, hq, hk, d, cols = 64, 8, 2, 128, 12
+    lens0 = [700, 1, 0, 768, 333, 64]
+    kc, vc, bt = _paged([cols * page] * len(lens0), page, hk, d, seed=800, cols=cols)
+    q = randn((len(lens0), 1, hq, d), 803).to(DEV)
+    kcd, vcd, btd = kc.to(DEV), vc.to(DEV), bt.to(DEV)
+    max_keys = cols * page
+    scale = 1.0 / math.sqrt(d)
+    lens = torch.tensor(lens0, dtype=torch.int32, device=DEV)
+    out = torch.empty_like(q)
+    lse = torch.empty((len(lens0), hq, 1), device=DEV)
+
+    def call():
+        _native.fwd_kvcache_noalloc(q, kcd, vcd, out, lse, lens, btd, None, None, max_keys,
+                                    scale, False, -1, -1, None)
+
+    call()                      # first call on the device: scratch address, kernel attributes
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    gen = torch.Generator().manual_seed(805)
+    for rep in range(4):
+        new = torch.randint(0, max_keys + 1, (len(lens0),), generator=gen, dtype=torch.int32)
+        lens.copy_(new)
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = torch.full_like(q, float("nan"))
+        ref_lse = torch.empty_like(lse)
+        _native.fwd_kvcache(q, kcd, vcd, ref, ref_lse, lens, btd, None, None, max_keys, scale,
+                            False, -1, -1, None)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {rep}: out"
+        assert torch.equal(lse.view(torch.int32), ref_lse.view(torch.int32)), f"replay {rep}: lse"
+
+
+def test_noalloc_fp32_takes_no_scratch():
+    # fp32 never splits a row's keys, so a shape whose 16-bit split workspace
+    # would exceed the scratch array runs (and equals fa_fwd_kvcache).
+    from flash_attn_triton import _native
+    B, hq, hk, d, page, cols = 512, 32, 8, 128, 256, 32
+    max_keys = page * cols
+    _, ws = _native.kvcache_plan(B, 1, hq, hk, d, max_keys, page)
+    assert ws > (16 << 20)
+    gen = torch.Generator().manual_seed(900)
+    lens = torch.randint(0, 2 * page + 1, (B,), generator=gen, dtype=torch.int32)
+    bt = torch.randint(0, 4, (B, cols), generator=gen, dtype=torch.int32)   # 4 shared pages
+    kc = randn((4, page, hk, d), 901, torch.float32).to(DEV)
+    vc = randn((4, page, hk, d), 902, torch.float32).to(DEV)
+    q = randn((B, 1, hq, d), 903, torch.float32).to(DEV)
+    args = (lens.to(DEV), bt.to(DEV), None, None, max_keys, 1.0 / math.sqrt(d), False, -1, -1, None)
+    got = torch.full_like(q, float("nan"))
+    _native.fwd_kvcache_noalloc(q, kc, vc, got, None, *args)
+    ref = torch.full_like(q, float("nan"))
+    _native.fwd_kvcache(q, kc, vc, ref, None, *args)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int32), ref.view(torch.int32))
