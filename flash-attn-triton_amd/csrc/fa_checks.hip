@@ -2,8 +2,9 @@
 // validates its arguments with (cache lengths, page tables, cache rows, left
 // pads), reduced in one launch.
 //
-// Workgroup i reduces array i (plus an optional elementwise addend) to its
-// minimum and maximum as int64 and writes them to minmax[2i], minmax[2i + 1].
+// Workgroup i reduces array i (plus an optional elementwise addend, or as the
+// differences of adjacent elements) to its minimum and maximum as int64 and
+// writes them to minmax[2i], minmax[2i + 1].
 // minmax may be pinned host memory, so the host reads the results after an
 // event on the stream without a separate device-to-host copy.
 #include <hip/hip_runtime.h>
@@ -19,8 +20,8 @@ constexpr int kThreads = 256;
 struct RangeJob {
   const void* a;   // int32 or int64 elements
   const void* b;   // nullable addend, int32 or int64
-  int64_t n;
-  int a_wide, b_wide;
+  int64_t n;       // values reduced: numel, or numel - 1 for differences
+  int a_wide, b_wide, diff;
 };
 
 struct RangeJobs {
@@ -37,8 +38,11 @@ __global__ __launch_bounds__(kThreads) void range_minmax_kernel(RangeJobs jobs) 
   const RangeJob j = jobs.job[blockIdx.x];
   int64_t lo = INT64_MAX, hi = INT64_MIN;
   for (int64_t i = threadIdx.x; i < j.n; i += kThreads) {
-    int64_t x = load_int(j.a, j.a_wide, i);
-    if (j.b) x += load_int(j.b, j.b_wide, i);
+    int64_t x = load_int(j.a, j.a_wide, i + (j.diff ? 1 : 0));
+    if (j.diff)
+      x -= load_int(j.a, j.a_wide, i);
+    else if (j.b)
+      x += load_int(j.b, j.b_wide, i);
     lo = x < lo ? x : lo;
     hi = x > hi ? x : hi;
   }
@@ -67,8 +71,8 @@ __global__ __launch_bounds__(kThreads) void range_minmax_kernel(RangeJobs jobs) 
 }  // namespace
 
 extern "C" int fa_check_ranges(int n, const void* const* a, const int* a_bytes,
-                               const void* const* b, const int* b_bytes, const int64_t* numel,
-                               int64_t* minmax, fa_stream_t stream) {
+                               const void* const* b, const int* b_bytes, const int* diff,
+                               const int64_t* numel, int64_t* minmax, fa_stream_t stream) {
   if (n < 1 || n > FA_MAX_RANGE_CHECKS)
     return fa_set_error(FA_ERR_INVALID, "fa_check_ranges: n must be in [1, FA_MAX_RANGE_CHECKS]");
   if (!a || !a_bytes || !numel || !minmax)
@@ -77,14 +81,16 @@ extern "C" int fa_check_ranges(int n, const void* const* a, const int* a_bytes,
     return fa_set_error(FA_ERR_INVALID, "fa_check_ranges: minmax must be 8-byte aligned");
   RangeJobs jobs{};
   for (int i = 0; i < n; ++i) {
-    const bool has_b = b && b[i];
+    const bool dif = diff && diff[i];
+    const bool has_b = !dif && b && b[i];
     if (!a[i] || numel[i] < 0 || (a_bytes[i] != 4 && a_bytes[i] != 8) ||
         (has_b && (!b_bytes || (b_bytes[i] != 4 && b_bytes[i] != 8))))
       return fa_set_error(FA_ERR_INVALID,
                           "fa_check_ranges: each array needs a pointer, a size >= 0 and 4- or "
                           "8-byte elements");
-    jobs.job[i] = RangeJob{a[i], has_b ? b[i] : nullptr, numel[i], a_bytes[i] == 8,
-                           has_b && b_bytes[i] == 8};
+    jobs.job[i] = RangeJob{a[i], has_b ? b[i] : nullptr,
+                           dif ? (numel[i] > 0 ? numel[i] - 1 : 0) : numel[i], a_bytes[i] == 8,
+                           has_b && b_bytes[i] == 8, dif ? 1 : 0};
   }
   // The results go to device memory or to pinned host memory, through the
   // address the device sees; pageable host memory would fault the kernel.

@@ -72,7 +72,7 @@ _SIGNATURES = {
                                  _i64p, _i64p, _i64p, _i64p, _int, _vp]),
     "fa_rotary_q": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _int, _i64, _i64, _i64,
                            _i64, _i64p, _i64p, _int, _vp]),
-    "fa_check_ranges": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "fa_check_ranges": (_int, [_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "fa_quant_k_int8": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _vp]),
     "fa_fwd_int8": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p,
                            _i64p, _f32, _int, _i64, _i64, _vp]),
@@ -359,25 +359,28 @@ def rotary_q(q, out, cache_seqlens, cache_leftpad, rotary_cos, rotary_sin,
 MAX_RANGE_CHECKS = 8
 
 
-def check_ranges(arrays, minmax) -> None:
+def check_ranges(arrays, minmax, diff=None) -> None:
     """min / max of each ``a`` (+ ``b``) of ``arrays`` = [(a, b or None), ...]
     (contiguous int32 / int64 device tensors, at most MAX_RANGE_CHECKS) into
     ``minmax`` (int64, 2 per array: pinned host or device memory), in one
-    launch on the current stream (fa_check_ranges)."""
+    launch on the current stream (fa_check_ranges).  ``diff[i]`` true: the
+    adjacent differences of ``a`` instead (``b`` must be None)."""
     lib = load()
     n = len(arrays)
-    for a, b in arrays:
+    diff = list(diff) if diff is not None else [False] * n
+    for (a, b), d in zip(arrays, diff):
         assert a.is_contiguous() and a.dtype in (torch.int32, torch.int64)
         assert b is None or (b.is_contiguous() and b.dtype in (torch.int32, torch.int64)
-                             and b.numel() == a.numel())
+                             and b.numel() == a.numel() and not d)
     assert minmax.dtype == torch.int64 and minmax.numel() >= 2 * n
     ptr_a = (ctypes.c_void_p * n)(*[a.data_ptr() for a, _ in arrays])
     bytes_a = (ctypes.c_int * n)(*[a.element_size() for a, _ in arrays])
     ptr_b = (ctypes.c_void_p * n)(*[None if b is None else b.data_ptr() for _, b in arrays])
     bytes_b = (ctypes.c_int * n)(*[4 if b is None else b.element_size() for _, b in arrays])
     numel = (ctypes.c_int64 * n)(*[a.numel() for a, _ in arrays])
+    diffs = (ctypes.c_int * n)(*[1 if d else 0 for d in diff])
     device = arrays[0][0].device
-    status = lib.fa_check_ranges(n, ptr_a, bytes_a, ptr_b, bytes_b, numel,
+    status = lib.fa_check_ranges(n, ptr_a, bytes_a, ptr_b, bytes_b, diffs, numel,
                                  ctypes.c_void_p(minmax.data_ptr()), _stream(device))
     _check(status, "fa_check_ranges")
 

@@ -469,9 +469,9 @@ def flash_attn_with_kvcache(
     except ValueError as exc:
         chk.fail(exc)
     if not launch_first:
-        alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
+        alibi_bits = chk.value_range(alibi.view(torch.int32)) if alibi is not None else None
         values = chk.flush()   # the one host synchronization of this call
-        if alibi is not None and not values[alibi_any]:
+        if alibi is not None and values[alibi_bits] == (0, 0):   # every slope +0.0
             alibi = None
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
@@ -679,12 +679,10 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         chk.fail(bad_start)
     # With seqused_* the reference re-derives that side's cu_seqlens from the
     # used counts (:563, :581), so its start/order/size checks always pass.
-    # Range checks on cu_seqlens slices and differences: one aminmax launch
-    # per tensor, shared by the checks that read it.
+    # Range checks on cu_seqlens slices and on its adjacent differences (the
+    # sequence lengths): all of them reduce in one fa_check_ranges launch.
     cu_q_first, cu_k_first = cu_seqlens_q[:1], cu_seqlens_k[:1]
     cu_q_last, cu_k_last = cu_seqlens_q[-1:], cu_seqlens_k[-1:]
-    len_q = cu_seqlens_q[1:] - cu_seqlens_q[:-1] if cu_seqlens_q.numel() > 1 else None
-    len_k = cu_seqlens_k[1:] - cu_seqlens_k[:-1] if cu_seqlens_k.numel() > 1 else None
     if seqused_q is None:
         chk.check_range(cu_q_first, 0, 0, bad_start)
     if seqused_k is None:
@@ -692,9 +690,9 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
     if cu_seqlens_q.numel() > 1:
         bad_order = ValueError("cu_seqlens arrays must be monotonically non-decreasing")
         if seqused_q is None:
-            chk.check_range(len_q, 0, None, bad_order)
-        if seqused_k is None and len_k is not None:
-            chk.check_range(len_k, 0, None, bad_order)
+            chk.check_range(cu_seqlens_q, 0, None, bad_order, diff=True)
+        if seqused_k is None and cu_seqlens_k.numel() > 1:
+            chk.check_range(cu_seqlens_k, 0, None, bad_order, diff=True)
     bad_size = ValueError("cu_seqlens values exceed the packed tensor sizes")
     if seqused_q is None:
         chk.check_range(cu_q_last, None, q.shape[0], bad_size)
@@ -745,11 +743,15 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                         ValueError("cu_seqlens arrays must cover the packed q and KV tensors"))
     if cu_seqlens_q.numel() < 2:
         chk.fail(ValueError("cu_seqlens arrays must describe at least one sequence"))
-    used_len_q = seqused_q if seqused_q is not None else len_q
-    used_len_k = seqused_k if seqused_k is not None else len_k
     bad_max = ValueError("max sequence lengths must cover every packed sequence")
-    chk.check_range(used_len_q, None, max_seqlen_q, bad_max)
-    chk.check_range(used_len_k, None, max_seqlen_k, bad_max)
+    if seqused_q is not None:
+        chk.check_range(seqused_q, None, max_seqlen_q, bad_max)
+    else:
+        chk.check_range(cu_seqlens_q, None, max_seqlen_q, bad_max, diff=True)
+    if seqused_k is not None:
+        chk.check_range(seqused_k, None, max_seqlen_k, bad_max)
+    else:
+        chk.check_range(cu_seqlens_k, None, max_seqlen_k, bad_max, diff=True)
     out_rows = chk.value(seqused_q.sum()) if seqused_q is not None else None
     if max_seqlen_q == 0 or max_seqlen_k == 0:
         values = chk.flush()
@@ -759,7 +761,9 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
         alibi = _normalize_alibi(alibi_slopes, batch_size, q.shape[1], q.device)
     except ValueError as exc:
         chk.fail(exc)
-    alibi_any = chk.value((alibi != 0).any()) if alibi is not None else None
+    # Any nonzero slope?  The fp32 bit patterns' range (one array of the
+    # range-check launch): all slopes +0.0 iff min and max are both 0.
+    alibi_bits = chk.value_range(alibi.view(torch.int32)) if alibi is not None else None
     if return_attn_probs:
         chk.flush()
         if paged or seqused_q is not None or seqused_k is not None:
@@ -770,7 +774,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
                                             window_size, softcap, alibi)
     values = chk.flush()   # the one host synchronization of this call
     seed = new_dropout_seed() if dropout_p > 0.0 else 0
-    use_alibi = alibi is not None and bool(values[alibi_any])
+    use_alibi = alibi is not None and values[alibi_bits] != (0, 0)
     if softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     cu_out = None

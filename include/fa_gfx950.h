@@ -335,13 +335,16 @@ int fa_rotary_q(const void* q, void* out, const int32_t* cache_seqlens,
  * integers of a_bytes[i] (4 or 8) bytes; b[i] (b or b[i] may be NULL) an
  * addend of the same length and b_bytes[i] bytes; minmax[2i] and minmax[2i+1]
  * receive min and max of a[i][j] + b[i][j] over j as int64 (INT64_MAX and
- * INT64_MIN for an empty array).  minmax is device memory or pinned host
+ * INT64_MIN for an empty array).  diff (nullable) selects, where diff[i] is
+ * nonzero, the differences of adjacent elements a[i][j+1] - a[i][j],
+ * j < numel[i] - 1, instead (b[i] ignored): the monotonicity check of
+ * cu_seqlens (flash_attn_interface.py:583-598).  minmax is device memory or pinned host
  * memory (checked with hipPointerGetAttributes; anything else is rejected),
  * so a host that passes pinned memory reads the results after an event on the
  * stream, with no copy.  a/b are device arrays.  One workgroup per array. */
 #define FA_MAX_RANGE_CHECKS 8
 int fa_check_ranges(int n, const void* const* a, const int* a_bytes, const void* const* b,
-                    const int* b_bytes, const int64_t* numel, int64_t* minmax,
+                    const int* b_bytes, const int* diff, const int64_t* numel, int64_t* minmax,
                     fa_stream_t stream);
 
 /* Per-token INT8 quantization of K (fp16), bit-exact with

@@ -48,3 +48,24 @@ def test_first_failing_check_in_queue_order_wins():
     chk.check(torch.tensor(False), IndexError("device"))
     with pytest.raises(RuntimeError):
         chk.fail(RuntimeError("host"))
+
+
+@pytest.mark.parametrize("dtype", [torch.int32, torch.int64])
+def test_adjacent_difference_ranges_and_value_ranges(dtype):
+    # cu_seqlens-style monotonicity: the differences of adjacent elements.
+    cu = torch.tensor([0, 3, 3, 10], dtype=dtype)
+    chk = Deferred()
+    chk.check_range(cu, 0, 7, ValueError("lengths"), diff=True)
+    chk.check_range(cu[:1], 0, 0, ValueError("start"), diff=True)   # no difference: skipped
+    i = chk.value_range(cu, diff=True)
+    j = chk.value_range(torch.tensor([5, -2, 9], dtype=dtype))
+    assert chk.flush() == [(0, 7), (-2, 9)]
+    chk.check_range(torch.tensor([0, 4, 2], dtype=dtype), 0, None, ValueError("order"), diff=True)
+    with pytest.raises(ValueError, match="order"):
+        chk.flush()
+    # An addend: lengths + left pads against a capacity.
+    chk.check_range(torch.tensor([4, 1], dtype=dtype), None, 5, ValueError("fit"),
+                    plus=torch.tensor([1, 5], dtype=torch.int64))
+    with pytest.raises(ValueError, match="fit"):
+        chk.flush()
+    assert (i, j) == (0, 1)

@@ -48,6 +48,19 @@ def test_check_ranges_kernel_min_max(wide):
     assert on_dev.cpu().tolist() == expect
 
 
+def test_check_ranges_adjacent_differences():
+    # The monotonicity form: min / max of a[j+1] - a[j], for both widths.
+    gen = torch.Generator().manual_seed(4)
+    for dt in (torch.int32, torch.int64):
+        for n in (2, 257, 3000):
+            a = torch.randint(-1000, 1000, (n,), generator=gen, dtype=torch.int64).cumsum(0).to(dt)
+            d = a[1:].long() - a[:-1].long()
+            host = torch.empty(4, dtype=torch.int64, pin_memory=True)
+            _native.check_ranges([(a.to(DEV), None), (a.to(DEV), None)], host, diff=[True, False])
+            torch.cuda.synchronize()
+            assert host.tolist() == [int(d.min()), int(d.max()), int(a.min()), int(a.max())]
+
+
 def test_check_ranges_rejects_pageable_host_memory():
     a = torch.arange(10, dtype=torch.int32, device=DEV)
     with pytest.raises(RuntimeError, match="pinned host memory"):
@@ -125,3 +138,48 @@ def test_batched_decode_checks_length_plus_leftpad():
     with pytest.raises(ValueError, match="valid lengths"):
         flash_attn_with_kvcache(q.to(DEV), kc, vc, cache_seqlens=(good + 1).to(DEV),
                                 cache_leftpad=pads.to(DEV))
+
+
+def test_varlen_checks_on_device_cu_seqlens():
+    # The varlen call's range checks (start, order, sizes, cover, max lengths)
+    # reduce in one launch; each failing case raises the reference's error
+    # before anything is launched.
+    from flash_attn_triton import flash_attn_varlen_func
+    H, D = 4, 64
+    lens = [5, 0, 70, 33]
+    T = sum(lens)
+    q, k, v = (randn((T, H, D), s).to(DEV) for s in (30, 31, 32))
+    cu = torch.tensor([0, 5, 5, 75, 108], dtype=torch.int32, device=DEV)
+    out = flash_attn_varlen_func(q, k, v, cu, cu, 70, 70, causal=True)
+    ref, _ = ora.attention_varlen(to_np(q.cpu()), to_np(k.cpu()), to_np(v.cpu()), cu.cpu().numpy(),
+                                  cu.cpu().numpy(), 1.0 / np.sqrt(D), True, (-1, -1), 0.0, None)
+    assert_close(to_np(out.cpu()), ref, ATOL[torch.float16], "varlen", torch.float16)
+    bad_order = torch.tensor([0, 5, 4, 75, 108], dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError, match="monotonically"):
+        flash_attn_varlen_func(q, k, v, bad_order, cu, 70, 70)
+    with pytest.raises(ValueError, match="start at zero"):
+        flash_attn_varlen_func(q, k, v, cu + 1, cu, 70, 70)
+    with pytest.raises(ValueError, match="exceed"):
+        flash_attn_varlen_func(q, k, v, cu, torch.tensor([0, 5, 5, 75, 109], dtype=torch.int32,
+                                                         device=DEV), 70, 70)
+    with pytest.raises(ValueError, match="max sequence lengths must cover"):
+        flash_attn_varlen_func(q, k, v, cu, cu, 69, 70)
+
+
+def test_varlen_zero_alibi_slopes_take_the_plain_path():
+    # All-+0.0 slopes (min and max of their bit patterns both 0) drop ALiBi;
+    # -0.0 keeps the ALiBi path, whose zero slopes give the same attention.
+    from flash_attn_triton import flash_attn_varlen_func
+    H, D = 4, 64
+    lens = [40, 90]
+    T = sum(lens)
+    q, k, v = (randn((T, H, D), s).to(DEV) for s in (40, 41, 42))
+    cu = torch.tensor([0, 40, 130], dtype=torch.int32, device=DEV)
+    plain = flash_attn_varlen_func(q, k, v, cu, cu, 90, 90, causal=True)
+    zero = flash_attn_varlen_func(q, k, v, cu, cu, 90, 90, causal=True,
+                                  alibi_slopes=torch.zeros(H, device=DEV))
+    neg0 = flash_attn_varlen_func(q, k, v, cu, cu, 90, 90, causal=True,
+                                  alibi_slopes=torch.full((H,), -0.0, device=DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(zero.view(torch.int16), plain.view(torch.int16))
+    assert (neg0.float() - plain.float()).abs().max().item() < 2e-3
