@@ -38,7 +38,11 @@
 // recency typical of real attention) scores grow towards the diagonal, and
 // walking upwards the running max moved past the rescale slack on about
 // 40 % of the tiles at BASELINE config 5 (64 multiplies of O^T each);
-// downwards the first tiles set it (measured 1 % faster there).
+// downwards the first tiles set it (measured 1 % faster there).  The tile
+// loads step running 64-bit bases and ring slots instead of forming each
+// tile's address from its index: the 64-bit products and slot divisions were
+// about 40 scalar instructions per tile, and dropping them made BASELINE
+// config 5 3 % faster (848 -> 822 us per launch on one MI355X).
 #pragma once
 
 #include "fa_fwd_kernel.h"
@@ -288,19 +292,36 @@ void prefill_kernel(const FwdParams p) {
   }
   const uint32_t k_ring_a = lds_address(k_ring) + IPW * w * 1024;
   const uint32_t v_ring_a = lds_address(v_ring) + IPW * w * 1024;
+  // issue_k and issue_v are each called for rel = 0, 1, 2, ... in order, so
+  // they step a running tile base down one tile and a running ring slot on
+  // per call (no per-tile 64-bit products or divisions).  Only the first
+  // (highest) tile can run past the sequence's last key: it takes the
+  // extent to that key, every lower tile exactly its BN rows, and tiles past
+  // J_all an empty resource.
+  const int n0_top = (t_end - 1) * BN;
+  const uint32_t k_top = J_all > 0 ? rows_extent(n0_top, Sk, p.k_ss, D) : 0u;
+  const uint32_t v_top = J_all > 0 ? rows_extent(n0_top, Sk, p.v_ss, D) : 0u;
+  const uint32_t k_full = rows_extent(0, BN, p.k_ss, D);
+  const uint32_t v_full = rows_extent(0, BN, p.v_ss, D);
+  const uint16_t* k_next = kg + (int64_t)n0_top * p.k_ss;
+  const uint16_t* v_next = vg + (int64_t)n0_top * p.v_ss;
+  const int64_t k_step = (int64_t)BN * p.k_ss, v_step = (int64_t)BN * p.v_ss;
+  int k_wslot = 0, v_wslot = 0;
   auto issue_k = [&](int rel) __attribute__((always_inline)) {
-    const int n0 = (t_end - 1 - rel) * BN;
-    const uint32_t ext = rel < J_all ? rows_extent(n0, Sk, p.k_ss, D) : 0u;
-    const u32x4 rs = make_rsrc_words(kg + (int64_t)(rel < J_all ? n0 : 0) * p.k_ss, ext);
-    const uint32_t dst = k_ring_a + (uint32_t)(rel % (kDma ? KS : 1)) * DTILEB;
+    const uint32_t ext = rel < J_all ? (rel == 0 ? k_top : k_full) : 0u;
+    const u32x4 rs = make_rsrc_words(k_next, ext);
+    k_next -= k_step;
+    const uint32_t dst = k_ring_a + (uint32_t)k_wslot * DTILEB;
+    k_wslot = k_wslot == (kDma ? KS : 1) - 1 ? 0 : k_wslot + 1;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, kd_off[i]);
   };
   auto issue_v = [&](int rel) __attribute__((always_inline)) {
-    const int n0 = (t_end - 1 - rel) * BN;
-    const uint32_t ext = rel < J_all ? rows_extent(n0, Sk, p.v_ss, D) : 0u;
-    const u32x4 rs = make_rsrc_words(vg + (int64_t)(rel < J_all ? n0 : 0) * p.v_ss, ext);
-    const uint32_t dst = v_ring_a + (uint32_t)(rel % (kDma ? KS - 1 : 1)) * DTILEB;
+    const uint32_t ext = rel < J_all ? (rel == 0 ? v_top : v_full) : 0u;
+    const u32x4 rs = make_rsrc_words(v_next, ext);
+    v_next -= v_step;
+    const uint32_t dst = v_ring_a + (uint32_t)v_wslot * DTILEB;
+    v_wslot = v_wslot == (kDma ? KS - 1 : 1) - 1 ? 0 : v_wslot + 1;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, vd_off[i]);
   };
