@@ -109,3 +109,62 @@ def test_persistent_causal_odd_groups_per_xcd():
     # keeps both row blocks of a pair in one group (the two-group pairing
     # needs an even count); 24 workgroups per XCD, two row blocks each.
     _case(1, 4096, 24, 24, True, seed=60)
+
+
+
+def test_persistent_causal_three_pairs_per_workgroup():
+    # B=3, H=32, S=4096: 12 groups per XCD, 96 row-block pairs over 32
+    # workgroups: three causal pairs (six row blocks) per workgroup.
+    _case(3, 4096, 32, 32, True, seed=70)
+
+
+def test_persistent_causal_gqa_bf16_long():
+    # S = 8192: 32 row blocks per group, grouped KV heads, bf16.
+    _case(2, 8192, 32, 8, True, dtype=torch.bfloat16, seed=80)
+
+
+def test_persistent_causal_repeats_streams_and_graph():
+    # Every row block is computed the same way whichever workgroup takes it
+    # and whenever it runs: repeated launches, launches on two streams at
+    # once, and replays of a captured graph (with eager launches between the
+    # replays) give bitwise the same output and LSE.
+    from flash_attn_triton.triton_kernel.attention_kernel import dense_forward
+    B, S, H, D = 4, 4096, 32, 128
+    q, k, v = (randn((B, S, H, D), s, torch.float16).to(DEV) for s in (91, 92, 93))
+    scale = 1.0 / math.sqrt(D)
+
+    def run():
+        return dense_forward(q, k, v, softmax_scale=scale, causal=True, return_lse=True)
+
+    out0, lse0 = run()
+    for _ in range(3):
+        out, lse = run()
+        assert torch.equal(out, out0) and torch.equal(lse, lse0)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    res = []
+    for st in (s1, s2, s1, s2):
+        with torch.cuda.stream(st):
+            res.append(run())
+    torch.cuda.synchronize()
+    for out, lse in res:
+        assert torch.equal(out, out0) and torch.equal(lse, lse0)
+    del res
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g, lse_g = run()
+    for _ in range(3):
+        out_g.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out0) and torch.equal(lse_g, lse0)
+        out, lse = run()
+        torch.cuda.synchronize()
+        assert torch.equal(out, out0) and torch.equal(lse, lse0)
