@@ -829,11 +829,17 @@ def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, dropout_p=0.0,
                                   causal=causal, **kwargs)
 
 
-class FlashSelfAttention(torch.nn.Module):
-    """FlashAttention-compatible self-attention module (reference :711-736)."""
+class _AttentionModule(torch.nn.Module):
+    """Shared configuration of the nn.Module front ends below.
 
-    def __init__(self, causal=False, softmax_scale=None, attention_dropout=0.0,
-                 window_size=(-1, -1), alibi_slopes=None, deterministic=False):
+    They mirror the reference's modules (flash_attn_interface.py:711-804):
+    the same constructor arguments and attribute names, dropout taken from a
+    ``torch.nn.Dropout`` member only in training mode, and a per-call
+    ``causal`` that overrides the constructor's.
+    """
+
+    def __init__(self, causal, softmax_scale, attention_dropout, window_size, alibi_slopes,
+                 deterministic):
         super().__init__()
         self.causal = causal
         self.softmax_scale = softmax_scale
@@ -841,53 +847,57 @@ class FlashSelfAttention(torch.nn.Module):
         self.window_size = window_size
         self.alibi_slopes = alibi_slopes
         self.deterministic = deterministic
+
+    def _options(self, causal):
+        """Keyword options shared by every call these modules make."""
+        return dict(dropout_p=self.drop.p if self.training else 0.0,
+                    softmax_scale=self.softmax_scale,
+                    causal=self.causal if causal is None else causal,
+                    window_size=self.window_size, alibi_slopes=self.alibi_slopes,
+                    deterministic=self.deterministic)
+
+
+class FlashSelfAttention(_AttentionModule):
+    """Self-attention on packed QKV: ``[B, S, 3, H, D]``, or ``[T, 3, H, D]``
+    with ``cu_seqlens`` / ``max_seqlen`` (reference :711-736)."""
+
+    def __init__(self, causal=False, softmax_scale=None, attention_dropout=0.0,
+                 window_size=(-1, -1), alibi_slopes=None, deterministic=False):
+        super().__init__(causal, softmax_scale, attention_dropout, window_size, alibi_slopes,
+                         deterministic)
 
     def forward(self, qkv, causal=None, cu_seqlens=None, max_seqlen=None):
-        dropout_p = self.drop.p if self.training else 0.0
-        causal = self.causal if causal is None else causal
-        if cu_seqlens is None:
-            return flash_attn_qkvpacked_func(qkv, dropout_p, self.softmax_scale, causal,
-                                             self.window_size, 0.0, self.alibi_slopes,
-                                             self.deterministic)
-        return flash_attn_varlen_qkvpacked_func(
-            qkv, cu_seqlens, max_seqlen, dropout_p, self.softmax_scale, causal,
-            window_size=self.window_size, alibi_slopes=self.alibi_slopes,
-            deterministic=self.deterministic)
+        opts = self._options(causal)
+        if cu_seqlens is not None:
+            return flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, **opts)
+        return flash_attn_qkvpacked_func(qkv, softcap=0.0, **opts)
 
 
-class FlashCrossAttention(torch.nn.Module):
-    """FlashAttention-compatible cross-attention module (reference :739-770)."""
+class FlashCrossAttention(_AttentionModule):
+    """Attention of ``q`` against packed ``kv``, split into K and V along
+    dim 2 in both forms as the reference does: ``[B, Sk, 2, Hk, D]`` dense,
+    ``[Tk, Hk, 2, D]`` with cu_seqlens.  The dense form takes grouped KV heads
+    natively outside training (reference :739-770)."""
 
     def __init__(self, causal=False, softmax_scale=None, attention_dropout=0.0,
                  window_size=(-1, -1), alibi_slopes=None, deterministic=False):
-        super().__init__()
-        self.causal = causal
-        self.softmax_scale = softmax_scale
-        self.drop = torch.nn.Dropout(attention_dropout)
-        self.window_size = window_size
-        self.alibi_slopes = alibi_slopes
-        self.deterministic = deterministic
+        super().__init__(causal, softmax_scale, attention_dropout, window_size, alibi_slopes,
+                         deterministic)
 
     def forward(self, q, kv, causal=None, cu_seqlens=None, max_seqlen=None,
                 cu_seqlens_k=None, max_seqlen_k=None):
-        dropout_p = self.drop.p if self.training else 0.0
-        causal = self.causal if causal is None else causal
+        opts = self._options(causal)
         k, v = kv.unbind(dim=2)
-        if cu_seqlens is None:
-            return flash_attn_func_cross(q, k, v, dropout_p, self.softmax_scale, causal,
-                                         use_native_gqa=not self.training, softcap=0.0,
-                                         alibi_slopes=self.alibi_slopes,
-                                         window_size=self.window_size,
-                                         deterministic=self.deterministic)
-        return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens_k, max_seqlen,
-                                      max_seqlen_k, dropout_p, self.softmax_scale, causal,
-                                      window_size=self.window_size,
-                                      alibi_slopes=self.alibi_slopes,
-                                      deterministic=self.deterministic)
+        if cu_seqlens is not None:
+            return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens_k, max_seqlen,
+                                          max_seqlen_k, **opts)
+        return flash_attn_func_cross(q, k, v, use_native_gqa=not self.training, softcap=0.0,
+                                     **opts)
 
 
 class FlashAttention(torch.nn.Module):
-    """Module wrapper of flash_attn_func (reference :773-804)."""
+    """``flash_attn_func`` as a module with a fixed dropout rate and scale,
+    dropout only in training mode (reference :773-804)."""
 
     def __init__(self, attention_dropout=0.0, softmax_scale=None):
         super().__init__()
@@ -895,9 +905,9 @@ class FlashAttention(torch.nn.Module):
         self.softmax_scale = softmax_scale
 
     def forward(self, q, k, v, causal=False, attn_bias=None):
-        return flash_attn_func(q, k, v, dropout_p=self.dropout_p if self.training else 0.0,
-                               softmax_scale=self.softmax_scale, causal=causal,
-                               attn_bias=attn_bias)
+        rate = self.dropout_p if self.training else 0.0
+        return flash_attn_func(q, k, v, dropout_p=rate, softmax_scale=self.softmax_scale,
+                               causal=causal, attn_bias=attn_bias)
 
 
 __all__ = [

@@ -207,3 +207,44 @@ def test_baseline_config_c2_sampled(causal):
     B, S, H, D = 4, 4096, 32, 128
     q, k, v = (randn((B, S, H, D), s) for s in (1, 2, 3))
     _sampled_rows_check(q, k, v, causal)
+
+
+def test_module_front_ends_match_the_functions():
+    # FlashSelfAttention / FlashCrossAttention / FlashAttention (reference
+    # flash_attn_interface.py:711-804) in eval mode equal the functional calls
+    # they stand for, dense and varlen (to fp16 rounding: the packed inputs
+    # are strided views, which may take another tile configuration); the
+    # per-call causal overrides the constructor's.
+    from flash_attn_triton import (FlashAttention, FlashCrossAttention, FlashSelfAttention,
+                                   flash_attn_func, flash_attn_varlen_func)
+
+    def _same(a, b):
+        torch.testing.assert_close(a.float(), b.float(), atol=2e-3, rtol=0)
+
+    B, S, H, Hk, D = 2, 96, 4, 2, 64
+    q = randn((B, S, H, D), 301).to(DEV)
+    k = randn((B, S, Hk, D), 302).to(DEV)
+    v = randn((B, S, Hk, D), 303).to(DEV)
+    kf = k.repeat_interleave(H // Hk, dim=2)
+    vf = v.repeat_interleave(H // Hk, dim=2)
+    self_attn = FlashSelfAttention(causal=True, softmax_scale=0.2).eval()
+    qkv = torch.stack([q, kf, vf], dim=2)
+    want = flash_attn_func(q, kf, vf, softmax_scale=0.2, causal=True)
+    _same(self_attn(qkv), want)
+    _same(self_attn(qkv, causal=False), flash_attn_func(q, kf, vf, softmax_scale=0.2, causal=False))
+    cross = FlashCrossAttention(window_size=(16, 0)).eval()
+    got = cross(q, torch.stack([k, v], dim=2))
+    _same(got, flash_attn_func(q, k, v, window_size=(16, 0), use_native_gqa=True))
+    full = FlashAttention(softmax_scale=0.3).eval()
+    _same(full(q, kf, vf, causal=True), flash_attn_func(q, kf, vf, softmax_scale=0.3, causal=True))
+    # Varlen forms on the same rows packed as [T, ...].
+    cu = torch.tensor([0, S, 2 * S], dtype=torch.int32, device=DEV)
+    qp, kp, vp = (t.reshape(B * S, *t.shape[2:]) for t in (q, kf, vf))
+    want_v = flash_attn_varlen_func(qp, kp, vp, cu, cu, S, S, softmax_scale=0.2, causal=True)
+    _same(self_attn(torch.stack([qp, kp, vp], dim=1), cu_seqlens=cu, max_seqlen=S), want_v)
+    want_v = flash_attn_varlen_func(qp, kp, vp, cu, cu, S, S, causal=True)
+    # The cross module splits K and V along dim 2 in both forms (as the
+    # reference does), so packed varlen kv is [T, Hk, 2, D].
+    _same(FlashCrossAttention(causal=True).eval()(
+        qp, torch.stack([kp, vp], dim=2), cu_seqlens=cu, max_seqlen=S, cu_seqlens_k=cu,
+        max_seqlen_k=S), want_v)
