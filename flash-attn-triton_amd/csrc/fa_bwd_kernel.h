@@ -639,11 +639,11 @@ void bwd_dkdv_kernel(const BwdParams p) {
     if (wl >= 0) need = need || p1 - wl > wk0;
     return need;
   };
-  // Divisor for the work-item split below: NM is 0 for key blocks no query
-  // row sees (J = 0), where only the empty prologue loads call these.
-  const int NMd = NM > 0 ? NM : 1;
-  auto head_of = [&](int it) { return kvh * p.group + it / NMd; };
-  auto m0_of = [&](int it) { return (m_begin + it % NMd) * BM; };
+  // Work item it is (query head kvh * group + it / NM, m-block m_begin + it % NM).
+  // The DMA stream and the products each visit the items in order, so each
+  // side keeps a running (m-block, head) pair instead of dividing per tile.
+  int ld_m = m_begin;               // m-block of the next tile to load
+  int mm_m = m_begin, mm_h = 0;     // m-block and head-in-group of the next tile to compute
 
   // ------------------------------------------------------------ DMA stream
   // Waves [0, NW/2) copy Q tiles, the others dO tiles; each wave writes
@@ -663,23 +663,48 @@ void bwd_dkdv_kernel(const BwdParams p) {
   const uint32_t f_voff = (uint32_t)lane * (uint32_t)(p.lse_ss * 4);
   const uint32_t x_lds = lds_address(smem_b) + (load_q ? 0 : NS * TILEB) + j0 * 1024;
   const uint32_t f_lds = lds_address(smem_b) + 2 * NS * TILEB + (w & 1) * NS * FB;
-  auto issue = [&](int it, int stage) {   // tile `it` into stage it % NS; past J an empty load
-    const bool live = it < J;
-    const int hq = head_of(live ? it : 0), m0 = m0_of(live ? it : 0);
-    const uint16_t* src = (load_q ? static_cast<const uint16_t*>(p.q) +
-                                        row_base(p, p.q_sb, p.q_ss, p.q_sh, b, hq, qs)
-                                  : static_cast<const uint16_t*>(p.dout) +
-                                        row_base(p, p.do_sb, p.do_ss, p.do_sh, b, hq, qs)) +
-                          (int64_t)m0 * x_ss;
-    const u32x4 rs = make_rsrc_words(src, live ? rows_extent(m0, Sq, x_ss, D) : 0u);
+  // Running DMA sources: the next tile's first Q / dO row and LSE / delta
+  // entry, and the byte extents from there to the end of the head's rows.
+  // A step moves one m-block down; after the last m-block of a head the
+  // pointers move to the first m-block of the next head.  Every live tile has
+  // m0 < q_hi <= Sq, so its extents are positive.
+  const int64_t x_sh = load_q ? p.q_sh : p.do_sh;
+  const uint16_t* x_run =
+      (load_q ? static_cast<const uint16_t*>(p.q) + row_base(p, p.q_sb, p.q_ss, p.q_sh, b, kvh * p.group, qs)
+              : static_cast<const uint16_t*>(p.dout) +
+                    row_base(p, p.do_sb, p.do_ss, p.do_sh, b, kvh * p.group, qs)) +
+      (int64_t)m_begin * BM * x_ss;
+  const float* f_run = ((w & 1) ? p.delta : p.lse) +
+                       row_base(p, p.lse_sb, p.lse_ss, p.lse_sh, b, kvh * p.group, qs) +
+                       (int64_t)m_begin * BM * p.lse_ss;
+  const int64_t x_mstep = (int64_t)BM * x_ss, f_mstep = (int64_t)BM * p.lse_ss;
+  const int64_t x_hstep = x_sh - (int64_t)(NM - 1) * x_mstep;
+  const int64_t f_hstep = p.lse_sh - (int64_t)(NM - 1) * f_mstep;
+  const int64_t x_ext0 = ((int64_t)(Sq - 1 - m_begin * BM) * x_ss + D) * 2;
+  const int64_t f_ext0 = ((int64_t)(Sq - 1 - m_begin * BM) * p.lse_ss + 1) * 4;
+  int64_t x_ext = x_ext0, f_ext = f_ext0;
+  int ld_left = J;                  // live tiles not yet loaded
+  auto clamp32 = [](int64_t v) { return v > 0xffffffffll ? 0xffffffffu : (uint32_t)v; };
+  auto issue = [&](int stage) {     // the next tile into `stage`; past J an empty load
+    const bool live = ld_left > 0;
+    const u32x4 rs = make_rsrc_words(x_run, live ? clamp32(x_ext) : 0u);
     const uint32_t dst = x_lds + stage * TILEB;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) buf_load16_lds(rs, dst + i * 1024, voff[i]);
-    const float* fsrc = ((w & 1) ? p.delta : p.lse) +
-                        row_base(p, p.lse_sb, p.lse_ss, p.lse_sh, b, hq, qs) + (int64_t)m0 * p.lse_ss;
-    const uint32_t fext =
-        live && m0 < Sq ? (uint32_t)(((int64_t)(Sq - m0 - 1) * p.lse_ss + 1) * 4) : 0u;
-    buf_load4_lds(make_rsrc_words(fsrc, fext), f_lds + stage * FB, f_voff);
+    buf_load4_lds(make_rsrc_words(f_run, live ? clamp32(f_ext) : 0u), f_lds + stage * FB, f_voff);
+    --ld_left;
+    if (++ld_m == m_end) {
+      ld_m = m_begin;
+      x_run += x_hstep;
+      f_run += f_hstep;
+      x_ext = x_ext0;
+      f_ext = f_ext0;
+    } else {
+      x_run += x_mstep;
+      f_run += f_mstep;
+      x_ext -= 2 * x_mstep;
+      f_ext -= 4 * f_mstep;
+    }
   };
 
   f32x16 dk[NDB], dv[NDB];
@@ -729,14 +754,14 @@ void bwd_dkdv_kernel(const BwdParams p) {
   // 32-row block of S and dP first, then the products; the transposed Q / dO
   // reads of the dK / dV products are issued before the elementwise work,
   // which hides their latency.
-  auto tile_math = [&](int it, int stage, bool masked) {
+  auto tile_math = [&](int stage, bool masked) {
     const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem_b + stage * TILEB);
     const uint16_t* Ds = reinterpret_cast<const uint16_t*>(smem_b + (NS + stage) * TILEB);
     const float* Ls = reinterpret_cast<const float*>(smem_b + 2 * NS * TILEB + stage * FB);
     const float* Es = reinterpret_cast<const float*>(smem_b + 2 * NS * TILEB + (NS + stage) * FB);
-    const int hq = head_of(it), m0 = m0_of(it);
+    const int hq = kvh * p.group + mm_h, m0 = mm_m * BM;
     float slope = 0.f;
-    if (GENERIC && p.alibi != nullptr) slope = slopes_lds[it / NMd];
+    if (GENERIC && p.alibi != nullptr) slope = slopes_lds[mm_h];
     f32x16 s[NRB], dp[NRB];
     const uint8_t* Qb = reinterpret_cast<const uint8_t*>(Qs);
     const uint8_t* Db = reinterpret_cast<const uint8_t*>(Ds);
@@ -863,33 +888,37 @@ void bwd_dkdv_kernel(const BwdParams p) {
   // barrier publishes every wave's share of it.  The barrier also retires
   // the reads of tile it - 1, whose stage the next DMA refills.
 #pragma unroll
-  for (int s = 0; s < NS - 1; ++s) issue(s, s);
+  for (int s = 0; s < NS - 1; ++s) issue(s);
   // Straight-line body: a tile that holds no visible (row, key) pair for
   // this wave is computed anyway with the mask (its P is all zero).  A
   // branch around it would make the dK / dV accumulators a join value that
   // the compiler copies between register files on every iteration.  The
   // loop is unrolled by the stage count, so every stage base is a constant
   // that the LDS reads take as their immediate offset.
-  auto iteration = [&](int it, int stage) {
+  auto iteration = [&](int stage) {   // the next tile, held in `stage`
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPS));
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("s_barrier" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    issue(it + NS - 1, (stage + NS - 1) % NS);
-    tile_math(it, stage, wave_masks(m0_of(it)));
+    issue((stage + NS - 1) % NS);
+    tile_math(stage, wave_masks(mm_m * BM));
+    if (++mm_m == m_end) {
+      mm_m = m_begin;
+      ++mm_h;
+    }
   };
   if constexpr (STAGE) {
     static_assert(NS == 3, "the main loop is unrolled for three stages");
     int it = 0;
     for (; it + NS <= J; it += NS) {
-      iteration(it, 0);
-      iteration(it + 1, 1);
-      iteration(it + 2, 2);
+      iteration(0);
+      iteration(1);
+      iteration(2);
     }
-    if (it < J) iteration(it, 0);
-    if (it + 1 < J) iteration(it + 1, 1);
+    if (it < J) iteration(0);
+    if (it + 1 < J) iteration(1);
   } else {
-    for (int it = 0; it < J; ++it) iteration(it, it % NS);
+    for (int it = 0; it < J; ++it) iteration(it % NS);
   }
   // No DMA may still be writing LDS when the workgroup retires.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
