@@ -23,12 +23,14 @@
 //   each lane, so LSE and delta are per-lane scalars and dS^T is already the
 //   B operand of the dQ^T product (the same key permutation as the forward's
 //   P^T).  It also writes delta, computed from its dO and O rows.
-// * bwd_dkdv_kernel: a workgroup owns BN = 32*NW keys of one (batch, KV
-//   head); wave w owns 32 keys and keeps K and V of its keys in VGPRs.  Per
-//   tile of BM query rows (of every query head of the GQA group, so each dK /
-//   dV element has one writer): S = Q K^T, dP = dO V^T (A = Q / dO rows from
-//   LDS), P and dS in registers with one key per lane, dV^T += dO^T P and
-//   dK^T += Q^T dS (A = dO^T / Q^T by the transpose read).
+// * dK / dV: a workgroup owns 128 keys of one (batch, KV head), 32 per key
+//   group.  Per tile of query rows (of every query head of the GQA group, so
+//   each dK / dV element has one writer): S = Q K^T, dP = dO V^T (A = Q / dO
+//   rows from LDS), P and dS in registers with one key per lane, dV^T +=
+//   dO^T P and dK^T += Q^T dS (A = dO^T / Q^T by the transpose read).  Up to
+//   D = 128 each key group has two waves (bwd_dkdv_split_kernel,
+//   fa_bwd_split.h); at D = 256 one wave per group runs two passes
+//   (bwd_dkdv_kernel below).
 // Every LDS tile is read both row-wise (16-byte reads of one row per lane)
 // and transposed (ds_read_b64_tr_b16), so tiles are stored unpadded with an
 // XOR swizzle of their 16-byte chunks (swz_off) that keeps both patterns free
@@ -536,9 +538,10 @@ struct BwdDkvTile {
   static_assert(BM <= 64 && BM % 32 == 0, "one DMA lane per row for LSE / delta");
 };
 
-// PASS 0 accumulates dK and dV together; at D = 256 the two accumulators do
-// not fit beside K and V, so the launcher runs PASS 1 (dV only) and PASS 2 (dK
-// only), recomputing S in each.
+// dK / dV at D = 256, one wave per key group.  PASS 0 would accumulate dK and
+// dV together; at D = 256 the two accumulators do not fit beside K and V, so
+// the launcher runs PASS 1 (dV only) and PASS 2 (dK only), recomputing S in
+// each.
 template <class T, int D, int NW, int BM, int NS, bool GENERIC, int WPE, int PASS, bool VARLEN,
           bool BIAS = false>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
@@ -714,46 +717,9 @@ void bwd_dkdv_kernel(const BwdParams p) {
     dv[db] = f32x16{};
   }
 
-  // Operands are staged for head dims up to 128; at 256 the staged arrays
-  // would not fit beside the accumulators, so the products read LDS directly.
-  constexpr bool STAGE = D <= 128;
-  // Per-lane byte offsets within a stage, computed once (the Q and dO tiles
-  // share them): the row reads of S and dP (row rb*32 + c32, chunk 2 kc + g)
-  // and the two halves of each transposed read of dV and dK (tr_operand's
-  // addressing).  Recomputing the swizzle per tile cost ~90 integer VALU
-  // instructions per tile.
-  uint32_t rd_ofs[STAGE ? NRB * NKC : 1];
-  uint32_t tr_ofs[STAGE ? NCC * NDB * 2 : 1];
-  if constexpr (STAGE) {
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb)
-#pragma unroll
-      for (int kc = 0; kc < NKC; ++kc)
-        rd_ofs[rb * NKC + kc] = 2u * (uint32_t)swz_off<D>(rb * 32 + c32, 2 * kc + g);
-    const int j = lane & 15;
-#pragma unroll
-    for (int cc = 0; cc < NCC; ++cc)
-#pragma unroll
-      for (int db = 0; db < NDB; ++db) {
-        const int r = 16 * cc + 4 * g + (j >> 2);
-        const int d = db * 32 + 16 * (c32 >> 4) + 4 * (j & 3);
-        tr_ofs[(cc * NDB + db) * 2] = 2u * (uint32_t)(swz_off<D>(r, d >> 3) + (d & 7));
-        tr_ofs[(cc * NDB + db) * 2 + 1] = 2u * (uint32_t)(swz_off<D>(r + 8, d >> 3) + (d & 7));
-      }
-  }
-  auto tr_read = [&](const uint8_t* base, int cc, int db) {
-    const u32x2 lo = lds_read_tr16(reinterpret_cast<const uint16_t*>(base + tr_ofs[(cc * NDB + db) * 2]));
-    const u32x2 hi =
-        lds_read_tr16(reinterpret_cast<const uint16_t*>(base + tr_ofs[(cc * NDB + db) * 2 + 1]));
-    return u32x4{lo[0], lo[1], hi[0], hi[1]};
-  };
-
-  // One tile of BM query rows.  The operand reads are staged in registers and
-  // pinned ahead of the products that use them (left to itself the compiler
-  // waits out the LDS latency before every product): all A operands of a
-  // 32-row block of S and dP first, then the products; the transposed Q / dO
-  // reads of the dK / dV products are issued before the elementwise work,
-  // which hides their latency.
+  // One tile of BM query rows.  At D = 256 staged operand arrays would not
+  // fit beside the accumulators, so the products read their A operands
+  // straight from LDS.
   auto tile_math = [&](int stage, bool masked) {
     const uint16_t* Qs = reinterpret_cast<const uint16_t*>(smem_b + stage * TILEB);
     const uint16_t* Ds = reinterpret_cast<const uint16_t*>(smem_b + (NS + stage) * TILEB);
@@ -763,50 +729,16 @@ void bwd_dkdv_kernel(const BwdParams p) {
     float slope = 0.f;
     if (GENERIC && p.alibi != nullptr) slope = slopes_lds[mm_h];
     f32x16 s[NRB], dp[NRB];
-    const uint8_t* Qb = reinterpret_cast<const uint8_t*>(Qs);
-    const uint8_t* Db = reinterpret_cast<const uint8_t*>(Ds);
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       s[rb] = f32x16{};
       dp[rb] = f32x16{};
-      if constexpr (STAGE) {
-        u32x4 qa[NKC], da[NKC];
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
-          qa[kc] = *reinterpret_cast<const u32x4*>(Qb + rd_ofs[rb * NKC + kc]);
-          if (DO_DK) da[kc] = *reinterpret_cast<const u32x4*>(Db + rd_ofs[rb * NKC + kc]);
-        }
-#pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
-          s[rb] = T::mfma32(qa[kc], kreg[kc], s[rb]);
-          if (DO_DK) dp[rb] = T::mfma32(da[kc], vreg[kc], dp[rb]);
-        }
-        constexpr int NR = DO_DK ? 2 * NKC : NKC;
-        __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);   // LDS reads
-        __builtin_amdgcn_sched_group_barrier(0x008, NR, 0);   // MFMAs
-        __builtin_amdgcn_sched_barrier(0);
-      } else {
-#pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) {
-          const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
-          s[rb] = T::mfma32(load16(Qs + off), kreg[kc], s[rb]);
-          if (DO_DK) dp[rb] = T::mfma32(load16(Ds + off), vreg[kc], dp[rb]);
-        }
+      for (int kc = 0; kc < NKC; ++kc) {
+        const int off = swz_off<D>(rb * 32 + c32, 2 * kc + g);
+        s[rb] = T::mfma32(load16(Qs + off), kreg[kc], s[rb]);
+        if (DO_DK) dp[rb] = T::mfma32(load16(Ds + off), vreg[kc], dp[rb]);
       }
-    }
-    // Transposed operands of dV^T += dO^T P and dK^T += Q^T dS.
-    constexpr int NTA = STAGE ? NCC * NDB : 1;
-    u32x4 ta_v[DO_DV ? NTA : 1], ta_k[DO_DK ? NTA : 1];
-    if constexpr (STAGE) {
-#pragma unroll
-      for (int cc = 0; cc < NCC; ++cc) {
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          if (DO_DV) ta_v[cc * NDB + db] = tr_read(Db, cc, db);
-          if (DO_DK) ta_k[cc * NDB + db] = tr_read(Qb, cc, db);
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
     u32x4 pb[NCC], dsb[NCC];
     auto elementwise = [&](auto masked_c) {
@@ -871,13 +803,8 @@ void bwd_dkdv_kernel(const BwdParams p) {
     for (int cc = 0; cc < NCC; ++cc) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
-        if constexpr (STAGE) {
-          if (DO_DV) dv[db] = T::mfma32(ta_v[cc * NDB + db], pb[cc], dv[db]);
-          if (DO_DK) dk[db] = T::mfma32(ta_k[cc * NDB + db], dsb[cc], dk[db]);
-        } else {
-          if (DO_DV) dv[db] = T::mfma32(tr_operand<D>(Ds, lane, cc, db * 32), pb[cc], dv[db]);
-          if (DO_DK) dk[db] = T::mfma32(tr_operand<D>(Qs, lane, cc, db * 32), dsb[cc], dk[db]);
-        }
+        if (DO_DV) dv[db] = T::mfma32(tr_operand<D>(Ds, lane, cc, db * 32), pb[cc], dv[db]);
+        if (DO_DK) dk[db] = T::mfma32(tr_operand<D>(Qs, lane, cc, db * 32), dsb[cc], dk[db]);
       }
     }
   };
@@ -892,9 +819,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
   // Straight-line body: a tile that holds no visible (row, key) pair for
   // this wave is computed anyway with the mask (its P is all zero).  A
   // branch around it would make the dK / dV accumulators a join value that
-  // the compiler copies between register files on every iteration.  The
-  // loop is unrolled by the stage count, so every stage base is a constant
-  // that the LDS reads take as their immediate offset.
+  // the compiler copies between register files on every iteration.
   auto iteration = [&](int stage) {   // the next tile, held in `stage`
     __builtin_amdgcn_s_waitcnt(vmcnt_imm((NS - 2) * LPS));
     __builtin_amdgcn_sched_barrier(0);
@@ -907,19 +832,7 @@ void bwd_dkdv_kernel(const BwdParams p) {
       ++mm_h;
     }
   };
-  if constexpr (STAGE) {
-    static_assert(NS == 3, "the main loop is unrolled for three stages");
-    int it = 0;
-    for (; it + NS <= J; it += NS) {
-      iteration(0);
-      iteration(1);
-      iteration(2);
-    }
-    if (it < J) iteration(0);
-    if (it + 1 < J) iteration(1);
-  } else {
-    for (int it = 0; it < J; ++it) iteration(it % NS);
-  }
+  for (int it = 0; it < J; ++it) iteration(it % NS);
   // No DMA may still be writing LDS when the workgroup retires.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 

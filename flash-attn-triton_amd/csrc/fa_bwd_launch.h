@@ -4,14 +4,14 @@
 #pragma once
 
 #include "fa_bwd_kernel.h"
+#include "fa_bwd_split.h"
 
 namespace fa {
 
 // dQ: 4 waves x 32 query rows, 64-key tiles (32 from D = 128, where Q, dO and
-// the dQ^T accumulators take 128 registers; 256 at D = 256).  dK/dV: 4 waves
-// x 32 keys, 64 query rows per tile (32 from D = 128) in 3 LDS stages; the dK^T
-// / dV^T accumulators live in the accumulation registers, one wave per SIMD;
-// D = 256 accumulates dV and dK in two passes.
+// the dQ^T accumulators take 128 registers; 256 at D = 256).  dK/dV up to
+// D = 128: launch_dkdv_split below.  At D = 256: 4 waves x 32 keys, 32 query
+// rows per tile in 3 LDS stages, one wave per SIMD, dV and dK in two passes.
 template <int D> struct BwdCfg {
   static constexpr int DQ_NW = 4, DQ_BN = D >= 128 ? 32 : 64, DQ_NS = 3, DQ_WPE = D >= 256 ? 1 : 2;
   static constexpr int KV_NW = 4, KV_BM = D >= 128 ? 32 : 64, KV_NS = 3, KV_WPE = 1;
@@ -25,6 +25,30 @@ hipError_t launch_dkdv(BwdParams p, hipStream_t st) {
       bwd_dkdv_kernel<T, D, C::KV_NW, C::KV_BM, C::KV_NS, GEN, C::KV_WPE, PASS, VARLEN, BIAS>;
   // The ALiBi slope table (one float per query head of the group) follows the
   // stages; the attribute allows the largest table that still fits.
+  constexpr int kMaxLds = 160 * 1024;
+  static std::atomic<uint64_t> lds_devices{0};
+  hipError_t e = set_lds_limit(lds_devices, kern, kMaxLds);
+  if (e != hipSuccess) return e;
+  const int64_t lds = Tile::LDS_BYTES + (GEN && p.alibi != nullptr ? 4 * (int64_t)p.group : 0);
+  if (lds > kMaxLds) return hipErrorInvalidConfiguration;
+  p.n_blocks = (p.seqlen_k + Tile::BN - 1) / Tile::BN;
+  const int64_t total = (int64_t)p.n_blocks * p.heads_k * p.batch;
+  if (total > 0x7fffffff) return hipErrorInvalidConfiguration;
+  if (total <= 0) return hipSuccess;
+  p.total_blocks = (int)total;
+  hipLaunchKernelGGL(kern, dim3((unsigned)total), dim3(Tile::NT), (unsigned)lds, st, p);
+  return hipGetLastError();
+}
+
+// dK/dV for D <= 128: a P-wave and a dS-wave per group of 32 keys, 128 keys
+// per workgroup, 4 LDS stages.
+template <class T, int D, bool GEN, bool VARLEN, bool BIAS>
+hipError_t launch_dkdv_split(BwdParams p, hipStream_t st) {
+  // 32 query rows per tile from D = 128, and for the generic D = 64 kernels
+  // (whose elementwise step needs the registers); 64 below.
+  constexpr int BM = D >= 128 || (GEN && D >= 64) ? 32 : 64;
+  using Tile = BwdDkvSplitTile<T, D, BM, 4>;
+  auto kern = bwd_dkdv_split_kernel<T, D, BM, 4, GEN, VARLEN, BIAS>;
   constexpr int kMaxLds = 160 * 1024;
   static std::atomic<uint64_t> lds_devices{0};
   hipError_t e = set_lds_limit(lds_devices, kern, kMaxLds);
@@ -64,7 +88,7 @@ hipError_t launch_bwd_v(BwdParams p, hipStream_t st) {
     if (e != hipSuccess) return e;
     return launch_dkdv<T, D, GEN, 2, VARLEN, BIAS>(p, st);
   } else {
-    return launch_dkdv<T, D, GEN, 0, VARLEN, BIAS>(p, st);
+    return launch_dkdv_split<T, D, GEN, VARLEN, BIAS>(p, st);
   }
 }
 
