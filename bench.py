@@ -374,8 +374,8 @@ def make_copy(torch):
 KERNELS = {
     "dense_causal": ("fa::prefill_persist_kernel",),
     "dense": ("fa::prefill_persist_kernel",),
-    "bwd_causal": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
-    "bwd": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_kernel"),
+    "bwd_causal": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_split_kernel"),
+    "bwd": ("fa::bwd_dq_kernel", "fa::bwd_dkdv_split_kernel"),
     "int8_causal": ("fa::int8_persist_kernel",),
     "int8": ("fa::int8_persist_kernel",),
     "decode": ("fa::decode_kernel", "fa::decode_combine_kernel"),
