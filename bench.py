@@ -624,8 +624,9 @@ def run_cpu(torch, wl, budget):
         return wl["cpu"](budget)
 
 
-# The other targets of the metric, measured with the headline in the default run.
-EXTRAS = ("dense", "int8_causal", "int8", "decode", "varlen")
+# The other targets of the metric, and the backward of the headline
+# configuration, measured with the headline in the default run.
+EXTRAS = ("dense", "int8_causal", "int8", "decode", "varlen", "bwd_causal")
 
 
 def main():
